@@ -1,0 +1,88 @@
+// Shared device types and host helpers for the gfx950 kernels.
+//
+// Device code is written for CDNA4 (gfx950) only: wave64, MFMA
+// v_mfma_f32_32x32x16_f16, 160 KiB LDS per CU.  fp16 values are _Float16;
+// accumulation is always fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/dlm.h"
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace dlm {
+
+// ---------------------------------------------------------------------------
+// MFMA 32x32x16 f16 -> f32 (gfx950).  Operand layouts (wave64):
+//   A (32 rows x 16 k): lane l holds row (l & 31), k = 8*(l >> 5) + [0..7]
+//   B (16 k x 32 cols): lane l holds col (l & 31), k = 8*(l >> 5) + [0..7]
+//   C/D (32 x 32):      lane l holds col (l & 31); element e is
+//                       row 8*(e >> 2) + 4*(l >> 5) + (e & 3)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int mfma_row(int e, int lane) {
+  return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float gelu_erf_f(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+
+// Wave-wide reductions (wave64) through the cross-lane permute network.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace dlm
+
+// ---------------------------------------------------------------------------
+// Host-side error state shared by every C entry point.
+// ---------------------------------------------------------------------------
+namespace dlm {
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what, const char* file, int line);
+size_t& scratch_bytes_ref();
+void* scratch(size_t bytes, int slot, hipStream_t stream, int* status);
+}  // namespace dlm
+
+#define DLM_HIP(expr)                                                          \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) return dlm::hip_fail(e_, #expr, __FILE__, __LINE__); \
+  } while (0)
+
+#define DLM_LAUNCH_CHECK()                                                     \
+  do {                                                                         \
+    hipError_t e_ = hipGetLastError();                                         \
+    if (e_ != hipSuccess) return dlm::hip_fail(e_, "kernel launch", __FILE__, __LINE__); \
+  } while (0)
+
+#define DLM_REQUIRE(cond, msg)                                                 \
+  do {                                                                         \
+    if (!(cond)) return dlm::fail(DLM_ERR_INVALID_ARG, std::string(__func__) + ": " + (msg)); \
+  } while (0)
+
+static inline bool dlm_aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }

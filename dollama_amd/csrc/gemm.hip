@@ -1,0 +1,791 @@
+// MFMA GEMM core for gfx950 and everything built on it: linears with fused
+// bias / residual / GEGLU epilogues, and implicit-GEMM convolution on
+// channels-last activations (no im2col buffer).
+//
+// Replaces, by behaviour (not by code):
+//   - launch_gemm_fp16 -> cublasGemmEx (reference src/kernels/gemm.cu:425-434)
+//   - linear() = gemm + launch_bias_add_rowvec (src/infer/unet.cu:517-525)
+//   - launch_conv2d's im2col + GEMM + conv_bias_add_rows
+//     (src/kernels/conv2d.cu:362-448, :219-270, :171-182)
+//   - launch_geglu (src/kernels/geglu.cu:26-48) as a GEMM epilogue
+//   - launch_conv_bias_biasch / launch_conv_bias_residual
+//     (src/kernels/bias_add.cu:106-159) as conv epilogues.
+//
+// Design: C[M,N] = A[M,K] * W[N,K]^T with both operands K-contiguous, the
+// form MFMA consumes directly.  A workgroup owns a BM x BN output tile and 4
+// waves; each wave owns WM x WN built from 32x32 MFMA blocks.  K advances in
+// 64-wide slices staged in double-buffered LDS (row stride 72 halfs, which
+// puts the 8 rows a ds_read_b128 phase touches on distinct banks); the next
+// slice's global loads are issued before the current slice's MFMAs.
+// The A operand is produced by a loader: plain rows for linears, or the
+// implicit im2col gather (zero padding, channel concatenation of two
+// sources, nearest-2x upsampling, a second 1x1 segment) for convolutions.
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace dlm {
+
+constexpr int BK = 64;
+constexpr int LS = BK + 8;  // LDS row stride in halfs
+
+struct EpiArgs {
+  f16* y;
+  int ldy;
+  const f16* bias;
+  const f16* res;
+  int ldr;
+  float alpha;
+  float beta;
+  int act;
+  const f16* tbias;
+  int tbias_ld;
+  int rows_per_sample;  // output pixels per sample (conv), for tbias / NCHW out
+  int out_nchw;
+  int M;
+  int N;
+};
+
+// ---------------------------------------------------------------------------
+// A/B operand loaders.  Each thread owns V 16-byte vectors of a 64-wide K
+// slice: vector i covers row (tid/8 + i*NT/8), halfs [8*(tid%8), +8).
+// ---------------------------------------------------------------------------
+struct RowDesc {
+  const f16* p;
+  int ld;
+  int rows;
+  int K;
+
+  template <int BM, int NT>
+  struct Loader {
+    static constexpr int V = BM * BK / 8 / NT;
+    const f16* p;
+    int ld, rows, K, row0, cv;
+    __device__ Loader(const RowDesc& d, int r0, int tid)
+        : p(d.p), ld(d.ld), rows(d.rows), K(d.K), row0(r0 + tid / 8), cv(tid % 8) {}
+    __device__ __forceinline__ void load(int kt, u32x4 (&r)[V]) const {
+      const int k = kt * BK + cv * 8;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int row = row0 + i * (NT / 8);
+        if (row < rows && k < K)
+          r[i] = *reinterpret_cast<const u32x4*>(p + (size_t)row * ld + k);
+        else
+          r[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+};
+
+struct ConvParams {
+  // segment 0: KHxKW conv over concat(src0a[:C0a], src0b[:C0-C0a])
+  const f16* s0a;
+  const f16* s0b;
+  int C0a, C0, ld0a, ld0b;
+  int H, W;    // stored source resolution
+  int Hv, Wv;  // resolution the taps index (2H x 2W when upsampling)
+  int KW, stride, pad, up;
+  int K0;      // KH*KW*C0
+  // segment 1: 1x1 conv over concat(src1a[:C1a], src1b[:C1-C1a]) at output res
+  const f16* s1a;
+  const f16* s1b;
+  int C1a, C1, ld1a, ld1b;
+  int HoWo, Wo, M;
+  int generic;  // 1 when C0 is not a multiple of 64 (per-vector tap decode)
+};
+
+struct ConvDesc : ConvParams {
+  template <int BM, int NT>
+  struct Loader {
+    static constexpr int V = BM * BK / 8 / NT;
+    ConvParams d;
+    int pbase[V], ihb[V], iwb[V];
+    int row0, cv;
+    __device__ Loader(const ConvDesc& desc, int m0, int tid) : d(desc) {
+      cv = tid % 8;
+      row0 = m0 + tid / 8;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int m = row0 + i * (NT / 8);
+        if (m < d.M) {
+          const int n = m / d.HoWo;
+          const int p = m - n * d.HoWo;
+          const int oh = p / d.Wo;
+          const int ow = p - oh * d.Wo;
+          pbase[i] = n * d.H * d.W;
+          ihb[i] = oh * d.stride - d.pad;
+          iwb[i] = ow * d.stride - d.pad;
+        } else {
+          pbase[i] = -1;
+          ihb[i] = 0;
+          iwb[i] = 0;
+        }
+      }
+    }
+    __device__ __forceinline__ void load(int kt, u32x4 (&r)[V]) const {
+      const int k0 = kt * BK;
+      if (k0 < d.K0) {
+        if (!d.generic) {
+          // one tap per K slice (C0 % 64 == 0): tap / channel are wave-uniform
+          const int tap = k0 / d.C0;
+          const int c = k0 - tap * d.C0;
+          const int kh = tap / d.KW;
+          const int kw = tap - kh * d.KW;
+          const f16* src;
+          int ld, cc;
+          if (c < d.C0a) {
+            src = d.s0a; ld = d.ld0a; cc = c;
+          } else {
+            src = d.s0b; ld = d.ld0b; cc = c - d.C0a;
+          }
+          src += cc + cv * 8;
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            int ih = ihb[i] + kh, iw = iwb[i] + kw;
+            const bool ok = pbase[i] >= 0 && (unsigned)ih < (unsigned)d.Hv &&
+                            (unsigned)iw < (unsigned)d.Wv;
+            if (d.up) { ih >>= 1; iw >>= 1; }
+            if (ok)
+              r[i] = *reinterpret_cast<const u32x4*>(src + (size_t)(pbase[i] + ih * d.W + iw) * ld);
+            else
+              r[i] = u32x4{0u, 0u, 0u, 0u};
+          }
+        } else {
+          // small-channel convs (conv_in): decode the tap per 8-channel vector
+          const int k = k0 + cv * 8;
+          const bool kin = k < d.K0;
+          const int tap = kin ? k / d.C0 : 0;
+          const int c = k - tap * d.C0;
+          const int kh = tap / d.KW;
+          const int kw = tap - kh * d.KW;
+          const bool isa = c < d.C0a;
+          const f16* src = isa ? d.s0a + c : d.s0b + (c - d.C0a);
+          const int ld = isa ? d.ld0a : d.ld0b;
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            int ih = ihb[i] + kh, iw = iwb[i] + kw;
+            const bool ok = kin && pbase[i] >= 0 && (unsigned)ih < (unsigned)d.Hv &&
+                            (unsigned)iw < (unsigned)d.Wv;
+            if (d.up) { ih >>= 1; iw >>= 1; }
+            if (ok)
+              r[i] = *reinterpret_cast<const u32x4*>(src + (size_t)(pbase[i] + ih * d.W + iw) * ld);
+            else
+              r[i] = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      } else {
+        // segment 1 (1x1 over the block input at output resolution)
+        const int c = k0 - d.K0 + cv * 8;
+        const bool cin = c < d.C1;
+        const bool isa = c < d.C1a;
+        const f16* src = isa ? d.s1a + c : d.s1b + (c - d.C1a);
+        const int ld = isa ? d.ld1a : d.ld1b;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const int m = row0 + i * (NT / 8);
+          if (cin && m < d.M)
+            r[i] = *reinterpret_cast<const u32x4*>(src + (size_t)m * ld);
+          else
+            r[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  };
+};
+
+// ---------------------------------------------------------------------------
+// Tile scheduling: spread consecutive logical tiles over one XCD (the
+// hardware deals workgroup i to XCD i % 8, each XCD has its own L2), then
+// walk logical tiles in groups of 8 M-tiles so co-resident tiles share both
+// operand panels.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int q = total >> 3, r = total & 7;
+  const int x = bid & 7, slot = bid >> 3;
+  const int logical = x * q + (x < r ? x : r) + slot;
+  constexpr int GM = 8;
+  const int per_group = GM * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * GM;
+  const int gsz = min(tiles_m - first_m, GM);
+  const int rem = logical - g * per_group;
+  tm = first_m + rem % gsz;
+  tn = rem / gsz;
+}
+
+template <int BM, int BN, int WM, int WN, class Desc>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
+  constexpr int WAVES_N = BN / WN;
+  constexpr int NT = (BM / WM) * WAVES_N * 64;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AV = BM * BK / 8 / NT;
+  constexpr int BV = BN * BK / 8 / NT;
+  static_assert(AV * NT * 8 == BM * BK && BV * NT * 8 == BN * BK, "tile/thread mismatch");
+  constexpr int STAGE = (BM + BN) * LS;
+  __shared__ __attribute__((aligned(16))) f16 smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  int tmi, tni;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+
+  typename Desc::template Loader<BM, NT> al(ad, m0, tid);
+  RowDesc::Loader<BN, NT> bl(bd, n0, tid);
+  const int K = bd.K;
+  const int nk = (K + BK - 1) / BK;
+
+  u32x4 ra[AV], rb[BV];
+  al.load(0, ra);
+  bl.load(0, rb);
+  {
+    f16* As = smem;
+    f16* Bs = smem + BM * LS;
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int v = tid + i * NT;
+      *reinterpret_cast<u32x4*>(As + (v >> 3) * LS + (v & 7) * 8) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int v = tid + i * NT;
+      *reinterpret_cast<u32x4*>(Bs + (v >> 3) * LS + (v & 7) * 8) = rb[i];
+    }
+  }
+  __syncthreads();
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int a_row = wm * WM + (lane & 31);
+  const int b_row = wn * WN + (lane & 31);
+  const int k_off = (lane >> 5) * 8;
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      al.load(kt + 1, ra);
+      bl.load(kt + 1, rb);
+    }
+    const f16* As = smem + cur * STAGE;
+    const f16* Bs = As + BM * LS;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      f16x8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const f16x8*>(As + (a_row + i * 32) * LS + ks * 16 + k_off);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const f16x8*>(Bs + (b_row + j * 32) * LS + ks * 16 + k_off);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
+    }
+    if (more) {
+      f16* An = smem + (cur ^ 1) * STAGE;
+      f16* Bn = An + BM * LS;
+#pragma unroll
+      for (int i = 0; i < AV; ++i) {
+        const int v = tid + i * NT;
+        *reinterpret_cast<u32x4*>(An + (v >> 3) * LS + (v & 7) * 8) = ra[i];
+      }
+#pragma unroll
+      for (int i = 0; i < BV; ++i) {
+        const int v = tid + i * NT;
+        *reinterpret_cast<u32x4*>(Bn + (v >> 3) * LS + (v & 7) * 8) = rb[i];
+      }
+    }
+    __syncthreads();
+  }
+
+  // ------------------------------ epilogue ------------------------------
+  const int row_base = m0 + wm * WM;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * WN + j * 32 + (lane & 31);
+    const bool col_ok = col < ep.N;
+    const float bcol = (ep.bias && col_ok) ? (float)ep.bias[col] : 0.0f;
+    if (ep.act == DLM_ACT_GEGLU) {
+      // columns are interleaved in blocks of 16: lanes with (lane & 16) == 0
+      // hold the value column, their xor-16 partner the matching gate column
+      const bool is_val = (lane & 16) == 0;
+      const int ocol = (col >> 5) * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float h = acc[i][j][e] * ep.alpha + bcol;
+          const float g = __shfl_xor(h, 16, 64);
+          const int row = row_base + i * 32 + mfma_row(e, lane);
+          if (is_val && col_ok && row < ep.M) {
+            float v = h * gelu_erf_f(g);
+            if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol];
+            ep.y[(size_t)row * ep.ldy + ocol] = (f16)v;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = row_base + i * 32 + mfma_row(e, lane);
+          if (!col_ok || row >= ep.M) continue;
+          float v = acc[i][j][e] * ep.alpha + bcol;
+          int n = 0, p = row;
+          if (ep.rows_per_sample > 0) {
+            n = row / ep.rows_per_sample;
+            p = row - n * ep.rows_per_sample;
+          }
+          if (ep.tbias) v += (float)ep.tbias[(size_t)n * ep.tbias_ld + col];
+          if (ep.act == DLM_ACT_SILU) v = silu_f(v);
+          else if (ep.act == DLM_ACT_GELU) v = gelu_erf_f(v);
+          if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + col];
+          if (ep.out_nchw)
+            ep.y[((size_t)n * ep.N + col) * ep.rows_per_sample + p] = (f16)v;
+          else
+            ep.y[(size_t)row * ep.ldy + col] = (f16)v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side tile configuration choice and launch.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, class Desc>
+static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
+                      hipStream_t s) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, WM, WN, Desc>), dim3(tiles_m * tiles_n), dim3(NT),
+                     0, s, ad, bd, ep, tiles_m, tiles_n);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+static inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+template <class Desc>
+static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
+                       hipStream_t s) {
+  constexpr int kCUs = 256;
+  if (N <= 32) return launch_cfg<128, 32, 32, 32>(ad, bd, ep, M, N, s);
+  if (N <= 64) return launch_cfg<128, 64, 64, 32>(ad, bd, ep, M, N, s);
+  if (ceil_div(M, 128) * ceil_div(N, 128) >= kCUs)
+    return launch_cfg<128, 128, 64, 64>(ad, bd, ep, M, N, s);
+  if (ceil_div(M, 128) * ceil_div(N, 64) >= kCUs)
+    return launch_cfg<128, 64, 64, 32>(ad, bd, ep, M, N, s);
+  return launch_cfg<64, 64, 32, 32>(ad, bd, ep, M, N, s);
+}
+
+static EpiArgs make_epi(void* Y, int ldy, const void* bias, const void* R, int ldr, int M, int N,
+                        float alpha, float beta, int act) {
+  EpiArgs ep{};
+  ep.y = (f16*)Y;
+  ep.ldy = ldy;
+  ep.bias = (const f16*)bias;
+  ep.res = (const f16*)R;
+  ep.ldr = ldr;
+  ep.alpha = alpha;
+  ep.beta = beta;
+  ep.act = act;
+  ep.tbias = nullptr;
+  ep.tbias_ld = 0;
+  ep.rows_per_sample = 0;
+  ep.out_nchw = 0;
+  ep.M = M;
+  ep.N = N;
+  return ep;
+}
+
+int linear_impl(const void* X, int lda, const void* W, int ldw, const void* bias, const void* R,
+                int ldr, void* Y, int ldy, int M, int N, int K, float alpha, float beta, int act,
+                hipStream_t s) {
+  RowDesc ad{(const f16*)X, lda, M, K};
+  RowDesc bd{(const f16*)W, ldw, N, K};
+  EpiArgs ep = make_epi(Y, ldy, bias, R, ldr, M, N, alpha, beta, act);
+  return launch_gemm(ad, bd, ep, M, N, s);
+}
+
+// ---------------------------------------------------------------------------
+// Small helper kernels: layout transposes and weight repacking.
+// ---------------------------------------------------------------------------
+// out[n][p][c] (row stride C_pad) = in[n][c][p]; channels >= C are zero.
+__global__ void nchw_to_nhwc_kernel(const f16* __restrict__ in, f16* __restrict__ out, int C,
+                                    int HW, int C_pad) {
+  __shared__ f16 tile[32][33];
+  const int n = blockIdx.z;
+  const int c0 = blockIdx.y * 32, p0 = blockIdx.x * 32;
+  const int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
+  const f16* src = in + (size_t)n * C * HW;
+  for (int r = ty; r < 32; r += 8) {
+    const int c = c0 + r, p = p0 + tx;
+    tile[r][tx] = (c < C && p < HW) ? src[(size_t)c * HW + p] : (f16)0.0f;
+  }
+  __syncthreads();
+  f16* dst = out + (size_t)n * HW * C_pad;
+  for (int r = ty; r < 32; r += 8) {
+    const int p = p0 + r, c = c0 + tx;
+    if (p < HW && c < C_pad) dst[(size_t)p * C_pad + c] = tile[tx][r];
+  }
+}
+
+// out[n][c][p] = in[n][p][c] (row stride C_pad), c < C.
+__global__ void nhwc_to_nchw_kernel(const f16* __restrict__ in, f16* __restrict__ out, int C,
+                                    int HW, int C_pad) {
+  __shared__ f16 tile[32][33];
+  const int n = blockIdx.z;
+  const int c0 = blockIdx.y * 32, p0 = blockIdx.x * 32;
+  const int tx = threadIdx.x, ty = threadIdx.y;
+  const f16* src = in + (size_t)n * HW * C_pad;
+  for (int r = ty; r < 32; r += 8) {
+    const int p = p0 + r, c = c0 + tx;
+    tile[r][tx] = (p < HW && c < C) ? src[(size_t)p * C_pad + c] : (f16)0.0f;
+  }
+  __syncthreads();
+  f16* dst = out + (size_t)n * C * HW;
+  for (int r = ty; r < 32; r += 8) {
+    const int c = c0 + r, p = p0 + tx;
+    if (c < C && p < HW) dst[(size_t)c * HW + p] = tile[tx][r];
+  }
+}
+
+// out[co*ld + col0 + tap*Cin_pad + ci] = w[co][ci][tap] (zero for ci >= Cin)
+__global__ void conv_weight_pack_kernel(const f16* __restrict__ w, f16* __restrict__ out, int Cout,
+                                        int Cin, int taps, int Cin_pad, int ld, int col0) {
+  const long long total = (long long)Cout * taps * Cin_pad;
+  for (long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int ci = (int)(idx % Cin_pad);
+    const long long r = idx / Cin_pad;
+    const int tap = (int)(r % taps);
+    const int co = (int)(r / taps);
+    const f16 v = ci < Cin ? w[((size_t)co * Cin + ci) * taps + tap] : (f16)0.0f;
+    out[(size_t)co * ld + col0 + (size_t)tap * Cin_pad + ci] = v;
+  }
+}
+
+// GEGLU interleave: packed row 32q+s <- value row 16q+s (s<16) or gate row
+// d+16q+s-16 (s>=16).
+__global__ void geglu_pack_kernel(const f16* __restrict__ w, const f16* __restrict__ b,
+                                  f16* __restrict__ wo, f16* __restrict__ bo, int d, int K) {
+  const int r = blockIdx.x;  // packed row
+  const int q = r >> 5, s = r & 31;
+  const int src = s < 16 ? 16 * q + s : d + 16 * q + (s - 16);
+  for (int k = threadIdx.x; k < K; k += blockDim.x) wo[(size_t)r * K + k] = w[(size_t)src * K + k];
+  if (threadIdx.x == 0 && b && bo) bo[r] = b[src];
+}
+
+// [rows, cols] -> [cols, rows] plain transpose used to bring operands of
+// dlm_gemm_fp16 into K-contiguous form.
+__global__ void transpose_kernel(const f16* __restrict__ in, f16* __restrict__ out, int rows,
+                                 int cols, int ld_out) {
+  __shared__ f16 tile[32][33];
+  const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+  const int tx = threadIdx.x, ty = threadIdx.y;
+  for (int r = ty; r < 32; r += 8) {
+    const int rr = r0 + r, cc = c0 + tx;
+    tile[r][tx] = (rr < rows && cc < cols) ? in[(size_t)rr * cols + cc] : (f16)0.0f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int cc = c0 + r, rr = r0 + tx;
+    if (cc < cols && rr < rows) out[(size_t)cc * ld_out + rr] = tile[tx][r];
+  }
+}
+
+int nchw_to_nhwc(const void* in, void* out, int N, int C, int HW, int C_pad, hipStream_t s) {
+  dim3 grid((HW + 31) / 32, (std::max(C, C_pad) + 31) / 32, N);
+  hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
+                     HW, C_pad);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int nhwc_to_nchw(const void* in, void* out, int N, int C, int HW, int C_pad, hipStream_t s) {
+  dim3 grid((HW + 31) / 32, (C + 31) / 32, N);
+  hipLaunchKernelGGL(nhwc_to_nchw_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
+                     HW, C_pad);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int conv_weight_pack(const void* w, void* out, int Cout, int Cin, int KH, int KW, int Cin_pad,
+                     int ld, int col0, hipStream_t s) {
+  const long long total = (long long)Cout * KH * KW * Cin_pad;
+  const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(conv_weight_pack_kernel, dim3(blocks), dim3(256), 0, s, (const f16*)w,
+                     (f16*)out, Cout, Cin, KH * KW, Cin_pad, ld, col0);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Convolution (channels-last) host entry.
+// ---------------------------------------------------------------------------
+int conv_nhwc_impl(const dlm_conv_nhwc_args* a, hipStream_t s) {
+  const int Hv = a->upsample ? 2 * a->H : a->H;
+  const int Wv = a->upsample ? 2 * a->W : a->W;
+  const int Ho = (Hv + 2 * a->pad - a->KH) / a->stride + 1;
+  const int Wo = (Wv + 2 * a->pad - a->KW) / a->stride + 1;
+  const int C0 = a->C0a + a->C0b;
+  const int C1 = a->C1a + a->C1b;
+  ConvDesc d{};
+  d.s0a = (const f16*)a->src0a;
+  d.s0b = (const f16*)a->src0b;
+  d.C0a = a->C0a;
+  d.C0 = C0;
+  d.ld0a = a->ld0a;
+  d.ld0b = a->ld0b;
+  d.H = a->H;
+  d.W = a->W;
+  d.Hv = Hv;
+  d.Wv = Wv;
+  d.KW = a->KW;
+  d.stride = a->stride;
+  d.pad = a->pad;
+  d.up = a->upsample;
+  d.K0 = a->KH * a->KW * C0;
+  d.s1a = (const f16*)a->src1a;
+  d.s1b = (const f16*)a->src1b;
+  d.C1a = a->C1a;
+  d.C1 = C1;
+  d.ld1a = a->ld1a;
+  d.ld1b = a->ld1b;
+  d.HoWo = Ho * Wo;
+  d.Wo = Wo;
+  d.M = a->N * Ho * Wo;
+  d.generic = (C0 % BK != 0 || a->C0a % BK != 0) ? 1 : 0;
+  const int K = d.K0 + C1;
+  RowDesc bd{(const f16*)a->weight, a->ldw, a->Cout, K};
+  EpiArgs ep = make_epi(a->out, a->ldy, a->bias, a->residual, a->res_ld, d.M, a->Cout, 1.0f, 1.0f,
+                        a->act);
+  ep.tbias = (const f16*)a->tbias;
+  ep.tbias_ld = a->tbias_ld;
+  ep.rows_per_sample = d.HoWo;
+  ep.out_nchw = a->out_nchw;
+  return launch_gemm(d, bd, ep, d.M, a->Cout, s);
+}
+
+}  // namespace dlm
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace dlm;
+
+extern "C" {
+
+int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* bias,
+                    const void* R, int ldr, void* Y, int ldy, int M, int N, int K, float alpha,
+                    float beta, int act, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(X && W && Y, "NULL operand");
+  DLM_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K, lda and ldw must be multiples of 8");
+  DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
+  DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
+  DLM_REQUIRE(act >= DLM_ACT_NONE && act <= DLM_ACT_GELU, "unknown act");
+  if (act == DLM_ACT_GEGLU) {
+    DLM_REQUIRE(N % 32 == 0, "GEGLU needs N (interleaved value+gate columns) % 32 == 0");
+    DLM_REQUIRE(ldy >= N / 2, "ldy smaller than N/2");
+    DLM_REQUIRE(!R || ldr >= N / 2, "ldr smaller than N/2");
+  } else {
+    DLM_REQUIRE(ldy >= N, "ldy smaller than N");
+    DLM_REQUIRE(!R || ldr >= N, "ldr smaller than N");
+  }
+  return linear_impl(X, lda, W, ldw, bias, R, ldr, Y, ldy, M, N, K, alpha, beta, act,
+                     (hipStream_t)stream);
+}
+
+int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, float alpha,
+                  float beta, int transA, int transB, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(A && B && C, "NULL operand");
+  hipStream_t s = (hipStream_t)stream;
+  // The MFMA core consumes A as [M,K] and B as [N,K] (both K-contiguous).
+  // Other orientations are transposed once into scratch.
+  const int Kp = (K + 7) & ~7;
+  const f16* a_ptr = (const f16*)A;
+  const f16* b_ptr = (const f16*)B;
+  int lda = K, ldb = K;
+  int st = DLM_OK;
+  if (transA || Kp != K || !dlm_aligned16(A)) {
+    f16* t = (f16*)scratch((size_t)M * Kp * 2, 0, s, &st);
+    if (!t) return st;
+    DLM_HIP(hipMemsetAsync(t, 0, (size_t)M * Kp * 2, s));
+    if (transA) {  // A stored [K, M]
+      hipLaunchKernelGGL(transpose_kernel, dim3((M + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
+                         (const f16*)A, t, K, M, Kp);
+      DLM_LAUNCH_CHECK();
+    } else {
+      DLM_HIP(hipMemcpy2DAsync(t, (size_t)Kp * 2, A, (size_t)K * 2, (size_t)K * 2, M,
+                               hipMemcpyDeviceToDevice, s));
+    }
+    a_ptr = t;
+    lda = Kp;
+  }
+  if (!transB || Kp != K || !dlm_aligned16(B)) {
+    f16* t = (f16*)scratch((size_t)N * Kp * 2, 1, s, &st);
+    if (!t) return st;
+    DLM_HIP(hipMemsetAsync(t, 0, (size_t)N * Kp * 2, s));
+    if (!transB) {  // B stored [K, N]
+      hipLaunchKernelGGL(transpose_kernel, dim3((N + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
+                         (const f16*)B, t, K, N, Kp);
+      DLM_LAUNCH_CHECK();
+    } else {
+      DLM_HIP(hipMemcpy2DAsync(t, (size_t)Kp * 2, B, (size_t)K * 2, (size_t)K * 2, N,
+                               hipMemcpyDeviceToDevice, s));
+    }
+    b_ptr = t;
+    ldb = Kp;
+  }
+  return linear_impl(a_ptr, lda, b_ptr, ldb, nullptr, beta != 0.0f ? C : nullptr, N, C, N, M, N,
+                     Kp, alpha, beta, DLM_ACT_NONE, s);
+}
+
+int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias_out, int d, int K,
+                        void* stream) {
+  if (d <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(w && w_out, "NULL pointer");
+  DLM_REQUIRE(d % 16 == 0, "d must be a multiple of 16");
+  hipLaunchKernelGGL(geglu_pack_kernel, dim3(2 * d), dim3(256), 0, (hipStream_t)stream,
+                     (const f16*)w, (const f16*)bias, (f16*)w_out, (f16*)bias_out, d, K);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_conv_weight_pack_fp16(const void* w, void* out, int Cout, int Cin, int KH, int KW,
+                              int Cin_pad, int ld_out, int col0, void* stream) {
+  if (Cout <= 0 || Cin <= 0 || KH <= 0 || KW <= 0) return DLM_OK;
+  DLM_REQUIRE(w && out, "NULL pointer");
+  DLM_REQUIRE(Cin_pad >= Cin, "Cin_pad < Cin");
+  DLM_REQUIRE(ld_out >= col0 + KH * KW * Cin_pad, "ld_out too small");
+  return conv_weight_pack(w, out, Cout, Cin, KH, KW, Cin_pad, ld_out, col0, (hipStream_t)stream);
+}
+
+int dlm_nchw_to_nhwc_fp16(const void* in, void* out, int N, int C, int HW, int C_pad,
+                          void* stream) {
+  if (N <= 0 || C <= 0 || HW <= 0) return DLM_OK;
+  DLM_REQUIRE(in && out, "NULL pointer");
+  DLM_REQUIRE(C_pad >= C, "C_pad < C");
+  return nchw_to_nhwc(in, out, N, C, HW, C_pad, (hipStream_t)stream);
+}
+
+int dlm_nhwc_to_nchw_fp16(const void* in, void* out, int N, int C, int HW, int C_pad,
+                          void* stream) {
+  if (N <= 0 || C <= 0 || HW <= 0) return DLM_OK;
+  DLM_REQUIRE(in && out, "NULL pointer");
+  DLM_REQUIRE(C_pad >= C, "C_pad < C");
+  return nhwc_to_nchw(in, out, N, C, HW, C_pad, (hipStream_t)stream);
+}
+
+int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* a, void* stream) {
+  DLM_REQUIRE(a != nullptr, "args is NULL");
+  if (a->N <= 0 || a->H <= 0 || a->W <= 0 || a->Cout <= 0 || a->KH <= 0 || a->KW <= 0 ||
+      a->C0a <= 0)
+    return DLM_OK;
+  DLM_REQUIRE(a->src0a && a->weight && a->out, "NULL operand");
+  DLM_REQUIRE(a->stride >= 1 && a->pad >= 0, "bad stride/pad");
+  DLM_REQUIRE(!a->upsample || a->stride == 1, "upsample requires stride 1");
+  DLM_REQUIRE(a->C0b == 0 || a->src0b, "src0b NULL with C0b > 0");
+  DLM_REQUIRE(a->C1a == 0 || a->src1a, "src1a NULL with C1a > 0");
+  DLM_REQUIRE(a->C1b == 0 || a->src1b, "src1b NULL with C1b > 0");
+  const int C0 = a->C0a + a->C0b;
+  DLM_REQUIRE(a->C0a % 8 == 0 && a->C0b % 8 == 0 && a->C1a % 8 == 0 && a->C1b % 8 == 0,
+              "channel counts must be multiples of 8 (pad the input)");
+  DLM_REQUIRE(a->ld0a % 8 == 0 && a->ld0a >= a->C0a, "bad ld0a");
+  DLM_REQUIRE(a->C0b == 0 || (a->ld0b % 8 == 0 && a->ld0b >= a->C0b), "bad ld0b");
+  DLM_REQUIRE(a->C1a == 0 || (a->ld1a % 8 == 0 && a->ld1a >= a->C1a), "bad ld1a");
+  DLM_REQUIRE(a->C1b == 0 || (a->ld1b % 8 == 0 && a->ld1b >= a->C1b), "bad ld1b");
+  DLM_REQUIRE(a->C1a + a->C1b == 0 || (C0 % BK == 0 && a->C0a % BK == 0),
+              "the 1x1 segment needs 64-aligned segment-0 channels");
+  DLM_REQUIRE(a->C1b == 0 || a->C1a % BK == 0, "segment-1 split must be 64-aligned");
+  const int K = a->KH * a->KW * C0 + a->C1a + a->C1b;
+  DLM_REQUIRE(a->ldw % 8 == 0 && a->ldw >= K, "bad ldw");
+  DLM_REQUIRE(dlm_aligned16(a->src0a) && dlm_aligned16(a->weight) &&
+                  (!a->src0b || dlm_aligned16(a->src0b)) && (!a->src1a || dlm_aligned16(a->src1a)) &&
+                  (!a->src1b || dlm_aligned16(a->src1b)),
+              "operands must be 16-byte aligned");
+  const int Hv = a->upsample ? 2 * a->H : a->H;
+  const int Wv = a->upsample ? 2 * a->W : a->W;
+  const int Ho = (Hv + 2 * a->pad - a->KH) / a->stride + 1;
+  const int Wo = (Wv + 2 * a->pad - a->KW) / a->stride + 1;
+  if (Ho <= 0 || Wo <= 0) return DLM_OK;
+  DLM_REQUIRE(a->C1a + a->C1b == 0 || (Ho == a->H && Wo == a->W && !a->upsample),
+              "the 1x1 segment needs output resolution == input resolution");
+  DLM_REQUIRE(a->out_nchw || a->ldy >= a->Cout, "ldy < Cout");
+  DLM_REQUIRE(!a->residual || a->res_ld >= a->Cout, "res_ld < Cout");
+  DLM_REQUIRE(!a->tbias || a->tbias_ld >= a->Cout, "tbias_ld < Cout");
+  DLM_REQUIRE(a->act == DLM_ACT_NONE || a->act == DLM_ACT_SILU || a->act == DLM_ACT_GELU,
+              "conv act must be none/silu/gelu");
+  DLM_REQUIRE((long long)a->N * Hv * Wv * std::max(a->ld0a, a->ld0b) < (1LL << 31) &&
+                  (long long)a->N * Ho * Wo < (1LL << 31),
+              "tensor too large for 32-bit pixel indexing");
+  return conv_nhwc_impl(a, (hipStream_t)stream);
+}
+
+// Reference-layout conv (NCHW): stage the input channels-last (padded to a
+// multiple of 8 channels), repack the weight, run the implicit-GEMM kernel
+// and write NCHW straight from the epilogue.
+int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out, int N,
+                    int Cin, int H, int W, int Cout, int KH, int KW, int stride_h, int stride_w,
+                    int pad_h, int pad_w, int dilation_h, int dilation_w, void* stream) {
+  if (N <= 0 || Cin <= 0 || H <= 0 || W <= 0 || Cout <= 0 || KH <= 0 || KW <= 0) return DLM_OK;
+  if (stride_h <= 0 || stride_w <= 0 || dilation_h <= 0 || dilation_w <= 0) return DLM_OK;
+  DLM_REQUIRE(in && weight && out, "NULL operand");
+  if (dilation_h != 1 || dilation_w != 1)
+    return fail(DLM_ERR_UNSUPPORTED, "dlm_conv2d_fp16: dilation != 1 is not supported");
+  if (stride_h != stride_w || pad_h != pad_w)
+    return fail(DLM_ERR_UNSUPPORTED, "dlm_conv2d_fp16: anisotropic stride/pad not supported");
+  const int Ho = (H + 2 * pad_h - KH) / stride_h + 1;
+  const int Wo = (W + 2 * pad_w - KW) / stride_w + 1;
+  if (Ho <= 0 || Wo <= 0) return DLM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int Cp = (Cin + 7) & ~7;
+  const int K = KH * KW * Cp;
+  const int ldw = (K + 7) & ~7;
+  int st = DLM_OK;
+  f16* x = (f16*)scratch((size_t)N * H * W * Cp * 2, 2, s, &st);
+  if (!x) return st;
+  f16* wp = (f16*)scratch((size_t)Cout * ldw * 2, 3, s, &st);
+  if (!wp) return st;
+  if ((st = nchw_to_nhwc(in, x, N, Cin, H * W, Cp, s)) != DLM_OK) return st;
+  if ((st = conv_weight_pack(weight, wp, Cout, Cin, KH, KW, Cp, ldw, 0, s)) != DLM_OK) return st;
+  dlm_conv_nhwc_args a{};
+  a.src0a = x;
+  a.C0a = Cp;
+  a.ld0a = Cp;
+  a.N = N;
+  a.H = H;
+  a.W = W;
+  a.KH = KH;
+  a.KW = KW;
+  a.stride = stride_h;
+  a.pad = pad_h;
+  a.weight = wp;
+  a.ldw = ldw;
+  a.Cout = Cout;
+  a.bias = bias;
+  a.out = out;
+  a.ldy = Cout;
+  a.out_nchw = 1;
+  a.act = DLM_ACT_NONE;
+  return conv_nhwc_impl(&a, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,226 @@
+// Error state, device memory, streams and events of the C ABI.
+//
+// Replaces the reference's CUDA_CHECK / std::runtime_error reporting
+// (src/kernels/utils.cuh:17-45) with int status codes plus a thread-local
+// message, and its cudaMalloc/cudaMemcpy call sites
+// (src/core/allocator.hpp:16-130, src/kernels/device_arena.cu) with
+// dlm_malloc / dlm_memcpy.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+
+namespace dlm {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what, const char* file, int line) {
+  char buf[512];
+  std::snprintf(buf, sizeof(buf), "HIP error %d (%s) in %s at %s:%d", (int)e,
+                hipGetErrorString(e), what, file, line);
+  g_last_error = buf;
+  return e == hipErrorOutOfMemory ? DLM_ERR_OUT_OF_MEMORY : DLM_ERR_HIP;
+}
+
+// Grow-only per-device, per-slot scratch used by the reference-layout entry
+// points that stage NCHW <-> NHWC copies.  Growth synchronises the device
+// before freeing the old block, so stream-ordered users never see it vanish.
+namespace {
+struct ScratchSlot {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<std::vector<ScratchSlot>> g_scratch;  // [device][slot]
+}  // namespace
+
+void* scratch(size_t bytes, int slot, hipStream_t stream, int* status) {
+  (void)stream;
+  *status = DLM_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    *status = fail(DLM_ERR_HIP, "scratch: hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1);
+  auto& slots = g_scratch[dev];
+  if ((int)slots.size() <= slot) slots.resize(slot + 1);
+  ScratchSlot& s = slots[slot];
+  if (s.bytes >= bytes && s.ptr) return s.ptr;
+  if (s.ptr) {
+    if (hipDeviceSynchronize() != hipSuccess || hipFree(s.ptr) != hipSuccess) {
+      *status = fail(DLM_ERR_HIP, "scratch: release of old block failed");
+      return nullptr;
+    }
+    s.ptr = nullptr;
+    s.bytes = 0;
+  }
+  size_t want = bytes < 256 ? 256 : bytes;
+  want = (want + 0xFFFFF) & ~size_t(0xFFFFF);  // round to 1 MiB
+  if (hipMalloc(&s.ptr, want) != hipSuccess) {
+    s.ptr = nullptr;
+    *status = fail(DLM_ERR_OUT_OF_MEMORY, "scratch: hipMalloc of " + std::to_string(want) + " bytes failed");
+    return nullptr;
+  }
+  s.bytes = want;
+  return s.ptr;
+}
+
+}  // namespace dlm
+
+extern "C" {
+
+const char* dlm_last_error(void) { return dlm::g_last_error.c_str(); }
+
+int dlm_get_device_count(int* count) {
+  DLM_REQUIRE(count != nullptr, "count is NULL");
+  DLM_HIP(hipGetDeviceCount(count));
+  return DLM_OK;
+}
+
+int dlm_set_device(int device) {
+  DLM_HIP(hipSetDevice(device));
+  return DLM_OK;
+}
+
+int dlm_device_arch(char* buf, int buflen) {
+  DLM_REQUIRE(buf != nullptr && buflen > 0, "bad buffer");
+  int dev = 0;
+  DLM_HIP(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  DLM_HIP(hipGetDeviceProperties(&prop, dev));
+  std::snprintf(buf, (size_t)buflen, "%s", prop.gcnArchName);
+  return DLM_OK;
+}
+
+int dlm_malloc(void** ptr, size_t bytes) {
+  DLM_REQUIRE(ptr != nullptr, "ptr is NULL");
+  *ptr = nullptr;
+  if (bytes == 0) return DLM_OK;
+  DLM_HIP(hipMalloc(ptr, bytes));
+  return DLM_OK;
+}
+
+int dlm_free(void* ptr) {
+  if (ptr == nullptr) return DLM_OK;
+  DLM_HIP(hipFree(ptr));
+  return DLM_OK;
+}
+
+int dlm_host_malloc_pinned(void** ptr, size_t bytes) {
+  DLM_REQUIRE(ptr != nullptr, "ptr is NULL");
+  *ptr = nullptr;
+  if (bytes == 0) return DLM_OK;
+  DLM_HIP(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+  return DLM_OK;
+}
+
+int dlm_host_free_pinned(void* ptr) {
+  if (ptr == nullptr) return DLM_OK;
+  DLM_HIP(hipHostFree(ptr));
+  return DLM_OK;
+}
+
+static hipMemcpyKind to_kind(int kind) {
+  switch (kind) {
+    case 0: return hipMemcpyHostToDevice;
+    case 1: return hipMemcpyDeviceToHost;
+    case 2: return hipMemcpyDeviceToDevice;
+    default: return hipMemcpyDefault;
+  }
+}
+
+int dlm_memcpy(void* dst, const void* src, size_t bytes, int kind) {
+  if (bytes == 0) return DLM_OK;
+  DLM_REQUIRE(dst && src, "NULL pointer");
+  DLM_HIP(hipMemcpy(dst, src, bytes, to_kind(kind)));
+  return DLM_OK;
+}
+
+int dlm_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+  if (bytes == 0) return DLM_OK;
+  DLM_REQUIRE(dst && src, "NULL pointer");
+  DLM_HIP(hipMemcpyAsync(dst, src, bytes, to_kind(kind), (hipStream_t)stream));
+  return DLM_OK;
+}
+
+int dlm_memset_async(void* dst, int value, size_t bytes, void* stream) {
+  if (bytes == 0) return DLM_OK;
+  DLM_REQUIRE(dst != nullptr, "NULL pointer");
+  DLM_HIP(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+  return DLM_OK;
+}
+
+int dlm_device_synchronize(void) {
+  DLM_HIP(hipDeviceSynchronize());
+  return DLM_OK;
+}
+
+int dlm_mem_get_info(size_t* free_bytes, size_t* total_bytes) {
+  DLM_REQUIRE(free_bytes && total_bytes, "NULL pointer");
+  DLM_HIP(hipMemGetInfo(free_bytes, total_bytes));
+  return DLM_OK;
+}
+
+int dlm_stream_create(void** stream) {
+  DLM_REQUIRE(stream != nullptr, "stream is NULL");
+  hipStream_t s = nullptr;
+  DLM_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = (void*)s;
+  return DLM_OK;
+}
+
+int dlm_stream_destroy(void* stream) {
+  if (stream == nullptr) return DLM_OK;
+  DLM_HIP(hipStreamDestroy((hipStream_t)stream));
+  return DLM_OK;
+}
+
+int dlm_stream_synchronize(void* stream) {
+  DLM_HIP(hipStreamSynchronize((hipStream_t)stream));
+  return DLM_OK;
+}
+
+int dlm_event_create(void** event) {
+  DLM_REQUIRE(event != nullptr, "event is NULL");
+  hipEvent_t e = nullptr;
+  DLM_HIP(hipEventCreate(&e));
+  *event = (void*)e;
+  return DLM_OK;
+}
+
+int dlm_event_destroy(void* event) {
+  if (event == nullptr) return DLM_OK;
+  DLM_HIP(hipEventDestroy((hipEvent_t)event));
+  return DLM_OK;
+}
+
+int dlm_event_record(void* event, void* stream) {
+  DLM_REQUIRE(event != nullptr, "event is NULL");
+  DLM_HIP(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+  return DLM_OK;
+}
+
+int dlm_event_synchronize(void* event) {
+  DLM_REQUIRE(event != nullptr, "event is NULL");
+  DLM_HIP(hipEventSynchronize((hipEvent_t)event));
+  return DLM_OK;
+}
+
+int dlm_event_elapsed_ms(float* ms, void* start, void* stop) {
+  DLM_REQUIRE(ms && start && stop, "NULL argument");
+  DLM_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return DLM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,263 @@
+/*
+ * dlm.h — C ABI of the MI355X (gfx950) SDXL UNet dense-contraction hot path.
+ *
+ * Every entry point takes plain device pointers (fp16 = IEEE binary16 bit
+ * patterns, passed as void*), int dimensions, float scalars and an opaque
+ * stream handle (a hipStream_t passed as void*; NULL = the default stream).
+ * Every entry point returns an int status (DLM_OK == 0); on failure
+ * dlm_last_error() returns a thread-local description.  Work is enqueued on
+ * the stream and is stream-ordered; nothing synchronises unless its name says
+ * so.  The caller owns every buffer; no pointer is retained past a call.
+ *
+ * Dimension convention (reference src/kernels/conv2d.cu:762-771): a call with
+ * a non-positive dimension is a silent no-op that returns DLM_OK.
+ *
+ * Two layouts appear:
+ *   - reference layout entry points (dlm_conv2d_fp16, dlm_group_norm_fp16,
+ *     dlm_attention_fp16, ...) take exactly the reference kernel host API's
+ *     arguments and layouts (NCHW activations, [B,H,S,Dh] attention);
+ *   - channels-last entry points (*_nhwc_*, dlm_linear_fp16,
+ *     dlm_attention_strided_fp16) are the fused native forms that the UNet
+ *     driver uses: activations are [N,H,W,C] == [tokens,C], so the
+ *     transformer's sequence layout needs no transposes.
+ */
+#ifndef DLM_H
+#define DLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DLM_OK 0
+#define DLM_ERR_INVALID_ARG 1
+#define DLM_ERR_HIP 2
+#define DLM_ERR_OUT_OF_MEMORY 3
+#define DLM_ERR_UNSUPPORTED 4
+#define DLM_ERR_NOT_FOUND 5
+#define DLM_ERR_STATE 6
+
+/* ------------------------------------------------------------------ */
+/* Status, device, memory, streams, events                             */
+/* ------------------------------------------------------------------ */
+
+/* Replaces the CUDA_CHECK / std::runtime_error reporting of the reference
+ * (src/kernels/utils.cuh:17-45): returns the last error text of this thread. */
+const char* dlm_last_error(void);
+int dlm_get_device_count(int* count);
+int dlm_set_device(int device);
+/* Name of the GPU architecture of the current device (e.g. "gfx950"). */
+int dlm_device_arch(char* buf, int buflen);
+
+/* Device memory for the VRAM arena and allocators (reference
+ * src/core/allocator.hpp:16-130 CudaAllocator, src/kernels/device_arena.cu
+ * cudaMalloc/cudaFree call sites). */
+int dlm_malloc(void** ptr, size_t bytes);
+int dlm_free(void* ptr);
+int dlm_host_malloc_pinned(void** ptr, size_t bytes);
+int dlm_host_free_pinned(void* ptr);
+/* kind: 0 host->device, 1 device->host, 2 device->device, 3 default (UVA). */
+int dlm_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int dlm_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream);
+int dlm_memset_async(void* dst, int value, size_t bytes, void* stream);
+int dlm_device_synchronize(void);
+int dlm_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+
+int dlm_stream_create(void** stream);
+int dlm_stream_destroy(void* stream);
+int dlm_stream_synchronize(void* stream);
+int dlm_event_create(void** event);
+int dlm_event_destroy(void* event);
+int dlm_event_record(void* event, void* stream);
+int dlm_event_synchronize(void* event);
+int dlm_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ------------------------------------------------------------------ */
+/* Reference-layout kernel host API (1:1 with src/kernels/ *.cuh)       */
+/* ------------------------------------------------------------------ */
+
+/* conv2d, NCHW fp16, fp32 accumulate, optional bias (NULL = none).
+ * Replaces dollama::launch_conv2d (src/kernels/conv2d.cuh:38-40).
+ * Groups/dilation other than 1 return DLM_ERR_UNSUPPORTED. */
+int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out,
+                    int N, int Cin, int H, int W, int Cout, int KH, int KW,
+                    int stride_h, int stride_w, int pad_h, int pad_w,
+                    int dilation_h, int dilation_w, void* stream);
+
+/* C = alpha * op(A) op(B) + beta * C, row-major, fp16 in/out, fp32 accumulate.
+ * op(A) = [M,K], op(B) = [K,N].
+ * Replaces dollama::launch_gemm_fp16 (src/kernels/gemm.cuh:44-53). */
+int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K,
+                  float alpha, float beta, int transA, int transB, void* stream);
+
+/* GroupNorm over NCHW, fp32 statistics; fuse_silu = 1 applies x*sigmoid(x).
+ * Replaces launch_group_norm / launch_group_norm_mb / launch_group_norm_silu
+ * (src/kernels/groupnorm.cuh:51-108). */
+int dlm_group_norm_fp16(const void* in, const void* gamma, const void* beta, void* out,
+                        int N, int C, int H, int W, int num_groups, float eps,
+                        int fuse_silu, void* stream);
+
+/* LayerNorm over the last dim C of [rows, C]; gamma/beta may be NULL.
+ * Replaces launch_layer_norm (src/kernels/layernorm.cuh:51-57). */
+int dlm_layer_norm_fp16(const void* in, const void* gamma, const void* beta, void* out,
+                        int rows, int C, float eps, void* stream);
+
+/* O = softmax(scale * Q K^T) V, Q/O [B,H,Sq,Dh], K/V [B,H,Sk,Dh], fp32 softmax.
+ * Dh must be 64.  Replaces launch_attention / launch_attention_fast
+ * (src/kernels/attention.cuh:53-73). */
+int dlm_attention_fp16(const void* q, const void* k, const void* v, void* out,
+                       int B, int H, int Sq, int Sk, int Dh, float scale, void* stream);
+
+/* out[t, j] = in[t, j] * gelu_erf(in[t, d + j]); in [tokens, 2d], out [tokens, d].
+ * Replaces launch_geglu (src/kernels/geglu.cuh:42). */
+int dlm_geglu_fp16(const void* in, void* out, int tokens, int d, void* stream);
+
+/* Replace launch_silu / launch_gelu (src/kernels/activation.cuh:33-37). */
+int dlm_silu_fp16(const void* in, void* out, int n, void* stream);
+int dlm_gelu_fp16(const void* in, void* out, int n, void* stream);
+/* Replace launch_add / launch_upsample_nearest2x (src/kernels/elementwise.cuh:26-37). */
+int dlm_add_fp16(const void* a, const void* b, void* out, int n, void* stream);
+int dlm_upsample_nearest2x_fp16(const void* in, void* out, int N, int C, int H, int W,
+                                void* stream);
+/* Replace launch_bias_add_rowvec / launch_bias_add_channel /
+ * launch_conv_bias_biasch / launch_conv_bias_residual
+ * (src/kernels/bias_add.cuh:32-103).  Single rounding of the fp32 sum. */
+int dlm_bias_add_rowvec_fp16(const void* in, const void* bias, void* out, int tokens, int C,
+                             void* stream);
+int dlm_bias_add_channel_fp16(const void* in, const void* bias, void* out,
+                              int N, int C, int H, int W, void* stream);
+int dlm_conv_bias_biasch_fp16(const void* conv, const void* convbias, const void* tproj,
+                              void* out, int B, int Cout, int H, int W, void* stream);
+int dlm_conv_bias_residual_fp16(const void* conv, const void* convbias, const void* residual,
+                                void* out, int B, int Cout, int H, int W, void* stream);
+/* Sinusoidal embedding, cos first (flip_sin_to_cos), shift 0.
+ * Replaces launch_timestep_embedding (src/kernels/timeembed.cuh:44-47). */
+int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_period,
+                                void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Channels-last fused entry points (native forms used by the UNet)     */
+/* ------------------------------------------------------------------ */
+
+/* Epilogue activation codes. */
+#define DLM_ACT_NONE 0
+#define DLM_ACT_SILU 1
+/* GEGLU: the weight rows (and bias) are interleaved in blocks of 16
+ * (16 value rows, then the 16 matching gate rows, see dlm_geglu_pack_fp16);
+ * the output has N/2 columns: out = value * gelu_erf(gate). */
+#define DLM_ACT_GEGLU 2
+#define DLM_ACT_GELU 3
+
+/* Y[M, N] = act(alpha * X[M,K] W[N,K]^T + bias[N]) + beta * R[M, N]
+ * X row stride lda, W row stride ldw, Y row stride ldy, R row stride ldr
+ * (all in elements; all multiples of 8; K multiple of 8).
+ * bias and R may be NULL.  act = DLM_ACT_*.  For GEGLU, ldy counts output
+ * columns (N/2).  Replaces linear() = launch_gemm_fp16(transB) +
+ * launch_bias_add_rowvec (src/infer/unet.cu:517-525), with the residual add
+ * (launch_add, unet.cu:739) and launch_geglu (unet.cu:793) fused. */
+int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* bias,
+                    const void* R, int ldr, void* Y, int ldy, int M, int N, int K,
+                    float alpha, float beta, int act, void* stream);
+
+/* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
+ * diffusers stores them) into the 16-row interleave DLM_ACT_GEGLU expects. */
+int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias_out,
+                        int d, int K, void* stream);
+
+/* Repack a conv weight [Cout, Cin, KH, KW] into the channels-last GEMM form
+ * [Cout, KH, KW, Cin_pad] (Cin_pad >= Cin, zero filled), written at row
+ * stride ld_out elements (ld_out >= KH*KW*Cin_pad) starting at column col0. */
+int dlm_conv_weight_pack_fp16(const void* w, void* out, int Cout, int Cin, int KH, int KW,
+                              int Cin_pad, int ld_out, int col0, void* stream);
+
+/* Layout transposes: NCHW <-> NHWC (C_pad >= C channels in the NHWC side,
+ * extra channels zero filled on the way in). */
+int dlm_nchw_to_nhwc_fp16(const void* in, void* out, int N, int C, int HW, int C_pad,
+                          void* stream);
+int dlm_nhwc_to_nchw_fp16(const void* in, void* out, int N, int C, int HW, int C_pad,
+                          void* stream);
+
+/* Implicit-GEMM convolution on channels-last activations.
+ * Output pixel m = (n, oh, ow), output channel co:
+ *   y[m, co] = act( sum_seg sum_taps sum_ci x_seg[...] * w[co, k] + bias[co]
+ *                   + tbias[n * tbias_ld + co] ) + residual[m * res_ld + co]
+ * Segment 0 is a KHxKW conv (stride, pad) over the channel concatenation of
+ * src0 (C0a channels, row stride ld0a) and src0b (C0b channels, may be NULL)
+ * of spatial size H x W (or 2H x 2W nearest-upsampled when upsample = 1).
+ * Segment 1 (optional, C1a > 0) is a 1x1 stride-1 conv over the concatenation
+ * of src1a/src1b at the output resolution, accumulated into the same sum
+ * (the fused ResnetBlock2D conv_shortcut).  Weight rows are [Cout, Ktot] with
+ * Ktot = KH*KW*(C0a+C0b) + (C1a+C1b), channels-last per tap (see
+ * dlm_conv_weight_pack_fp16), row stride ldw.  Output channels-last with row
+ * stride ldy, or NCHW when out_nchw = 1. */
+typedef struct dlm_conv_nhwc_args {
+  const void* src0a; const void* src0b; int C0a; int C0b; int ld0a; int ld0b;
+  const void* src1a; const void* src1b; int C1a; int C1b; int ld1a; int ld1b;
+  int N; int H; int W; int KH; int KW; int stride; int pad; int upsample;
+  const void* weight; int ldw; int Cout;
+  const void* bias; const void* tbias; int tbias_ld;
+  const void* residual; int res_ld;
+  void* out; int ldy; int out_nchw; int act;
+} dlm_conv_nhwc_args;
+int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* args, void* stream);
+
+/* GroupNorm on channels-last [N, HW, C] (row stride ld_in / ld_out), C split
+ * into num_groups contiguous groups; optional second source (concatenation
+ * along channels: the first C_a channels from in_a, the rest from in_b).
+ * fuse_silu = 1 applies x*sigmoid(x).  workspace must hold
+ * dlm_group_norm_nhwc_workspace_bytes(N, C, HW) bytes. */
+size_t dlm_group_norm_nhwc_workspace_bytes(int N, int C, int HW);
+int dlm_group_norm_nhwc_fp16(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
+                             const void* gamma, const void* beta, void* out, int ld_out,
+                             int N, int HW, int C, int num_groups, float eps, int fuse_silu,
+                             void* workspace, void* stream);
+
+/* Strided flash attention: element (b, s, h, d) of Q is at
+ * q[b*q_sb + s*q_ss + h*q_sh + d] (likewise K, V, O); Dh = 64. */
+typedef struct dlm_attention_args {
+  const void* q; long long q_sb; long long q_ss; long long q_sh;
+  const void* k; long long k_sb; long long k_ss; long long k_sh;
+  const void* v; long long v_sb; long long v_ss; long long v_sh;
+  void* o; long long o_sb; long long o_ss; long long o_sh;
+  int B; int H; int Sq; int Sk; int Dh; float scale;
+} dlm_attention_args;
+int dlm_attention_strided_fp16(const dlm_attention_args* args, void* stream);
+
+/* SDXL conditioning inputs on the device (no host round trip, unlike the
+ * reference's D2H of time_ids, src/infer/unet.cu:999-1000):
+ * t_emb[b, 0:320] = sinusoid(timestep[b]) and
+ * add_in[b, 0:2816] = text_embeds[b, 0:1280] ++ sinusoid_256(time_ids[b*ids_bstride + i]), i<6. */
+int dlm_sdxl_embed_inputs_fp16(const float* timesteps, const void* text_embeds,
+                               const void* time_ids, int ids_bstride, void* t_emb,
+                               void* add_in, int B, void* stream);
+
+/* Skinny linear for M <= 16 rows (the time / add embedding MLPs and the
+ * per-resnet time_emb_proj): Y[m, n] = act(X'[m,:] . W[n,:] + bias[n]) where
+ * X' = silu(X) when silu_in = 1.  act: DLM_ACT_NONE or DLM_ACT_SILU.
+ * Y rows may accumulate: Y = Y + result when accumulate = 1. */
+int dlm_linear_small_fp16(const void* X, int ldx, const void* W, const void* bias, void* Y,
+                          int ldy, int M, int N, int K, int silu_in, int act, int accumulate,
+                          void* stream);
+
+/* Euler step fused with classifier-free guidance (reference
+ * src/infer/diffusion.cu:968-973 and src/infer/scheduler.hpp:112-143):
+ * eps = u + g (c - u) from noise [2, n] (cond slice first, uncond second),
+ * latent += eps * (sigma_next - sigma) in fp32, then the next model input
+ * model_in[0:n] = model_in[n:2n] = fp16(latent * in_scale), where in_scale =
+ * 1/sqrt(sigma_next^2 + 1) (scale_model_input of the next step). */
+int dlm_euler_cfg_step(float* latent, const void* noise, void* model_in, int n,
+                       float guidance, float sigma, float sigma_next, float in_scale,
+                       void* stream);
+
+/* model_in[c*n + i] = fp16(latent[i] * scale) for c < copies (the first
+ * step's scale_model_input, reference src/infer/scheduler.hpp:112-120). */
+int dlm_scale_latent_fp16(const float* latent, void* model_in, int n, float scale, int copies,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DLM_H */
