@@ -100,7 +100,7 @@ HIP_SIGNATURES = {
     "dlm_group_norm_nhwc_workspace_bytes": (c_size_t, [I, I, I]),
     "dlm_group_norm_nhwc_fp16": (I, [P, I, I, P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
     "dlm_attention_strided_fp16": (I, [POINTER(AttentionArgs), P]),
-    "dlm_sdxl_embed_inputs_fp16": (I, [P, P, P, I, P, P, I, P]),
+    "dlm_sdxl_embed_inputs_fp16": (I, [P, P, I, P, I, I, P, I, P, I, P]),
     "dlm_linear_small_fp16": (I, [P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),

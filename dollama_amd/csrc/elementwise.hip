@@ -95,18 +95,23 @@ __global__ void timestep_embedding_kernel(f16* out, float t, int dim, float log_
   sinusoid_one(out, t, dim, log_mp, blockIdx.x * blockDim.x + threadIdx.x);
 }
 
-// One block per batch row: t_emb[b, 0:320], add_in[b, 0:2816].
-__global__ void sdxl_embed_kernel(const float* timesteps, const f16* text, const f16* ids,
-                                  int ids_bstride, f16* t_emb, f16* add_in) {
+// One block per batch row: t_emb[b, 0:t_dim] = sinusoid(t_b), and
+// add_in[b] = text[b, 0:text_dim] ++ sinusoid_{id_dim}(ids[b*stride + i]), i < 6.
+__global__ void sdxl_embed_kernel(const float* timesteps, const f16* text, int text_dim,
+                                  const f16* ids, int ids_bstride, int id_dim, f16* t_emb,
+                                  int t_dim, f16* add_in) {
   const int b = blockIdx.x;
   const float log_mp = 9.210340371976184f;  // ln(10000)
   const int tid = threadIdx.x;
-  if (tid < 160) sinusoid_one(t_emb + b * 320, timesteps[b], 320, log_mp, tid);
-  f16* a = add_in + (size_t)b * 2816;
-  for (int i = tid; i < 1280; i += blockDim.x) a[i] = text[(size_t)b * 1280 + i];
-  for (int i = tid; i < 6 * 128; i += blockDim.x) {
-    const int k = i / 128, j = i % 128;
-    sinusoid_one(a + 1280 + k * 256, (float)ids[b * ids_bstride + k], 256, log_mp, j);
+  for (int j = tid; j < t_dim / 2; j += blockDim.x)
+    sinusoid_one(t_emb + (size_t)b * t_dim, timesteps[b], t_dim, log_mp, j);
+  const int add_dim = text_dim + 6 * id_dim;
+  f16* a = add_in + (size_t)b * add_dim;
+  for (int i = tid; i < text_dim; i += blockDim.x) a[i] = text[(size_t)b * text_dim + i];
+  const int hd = id_dim / 2;
+  for (int i = tid; i < 6 * hd; i += blockDim.x) {
+    const int k = i / hd, j = i % hd;
+    sinusoid_one(a + text_dim + k * id_dim, (float)ids[b * ids_bstride + k], id_dim, log_mp, j);
   }
 }
 
@@ -287,15 +292,16 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
   return DLM_OK;
 }
 
-int dlm_sdxl_embed_inputs_fp16(const float* timesteps, const void* text_embeds,
-                               const void* time_ids, int ids_bstride, void* t_emb, void* add_in,
-                               int B, void* stream) {
+int dlm_sdxl_embed_inputs_fp16(const float* timesteps, const void* text_embeds, int text_dim,
+                               const void* time_ids, int ids_bstride, int id_dim, void* t_emb,
+                               int t_dim, void* add_in, int B, void* stream) {
   if (B <= 0) return DLM_OK;
   DLM_REQUIRE(timesteps && text_embeds && time_ids && t_emb && add_in, "NULL pointer");
-  DLM_REQUIRE(ids_bstride >= 0, "ids_bstride must be >= 0");
+  DLM_REQUIRE(ids_bstride >= 0 && text_dim > 0 && id_dim > 0 && t_dim > 0, "bad dims");
+  DLM_REQUIRE(t_dim % 2 == 0 && id_dim % 2 == 0, "embedding dims must be even");
   hipLaunchKernelGGL(sdxl_embed_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, timesteps,
-                     (const f16*)text_embeds, (const f16*)time_ids, ids_bstride, (f16*)t_emb,
-                     (f16*)add_in);
+                     (const f16*)text_embeds, text_dim, (const f16*)time_ids, ids_bstride, id_dim,
+                     (f16*)t_emb, t_dim, (f16*)add_in);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

@@ -34,7 +34,10 @@ static GnPlan gn_plan(int N, int C, int HW) {
   p.R = std::max(1, 256 / p.S);
   while (p.S * p.R > 1024 && p.R > 1) --p.R;
   p.threads = p.S * p.R;
-  const int target = std::max(1, 512 / std::max(1, N));
+  // chunking depends on HW only, so each sample's statistics are computed
+  // identically whatever the batch size (B=2 == 2 x B=1, bit for bit)
+  (void)N;
+  const int target = 256;
   p.chunk = std::max(p.R * 4, (HW + target - 1) / target);
   p.chunks = (HW + p.chunk - 1) / p.chunk;
   return p;
@@ -51,11 +54,15 @@ __device__ __forceinline__ void load8(const f16* p, float (&v)[8]) {
   for (int i = 0; i < 8; ++i) v[i] = (float)x[i];
 }
 
-// partial[n][chunk][c] = (mean_c, M2_c) over the chunk's pixels
+// partial[n][chunk][g] = (mean, M2) of group g over the chunk's pixels.
+// Per-channel sums are shifted by the chunk's first pixel, reduced over the R
+// rows in LDS, turned into per-channel (mean, M2) and combined per group with
+// the equal-count form of Chan's formula.
 __global__ void gn_partial_kernel(const f16* __restrict__ a, int Ca, int lda,
-                                  const f16* __restrict__ b, int ldb, int HW, int C, int chunk,
-                                  int chunks, int S, int R, float2* __restrict__ partial) {
-  extern __shared__ float2 red[];  // [R][C]
+                                  const f16* __restrict__ b, int ldb, int HW, int C, int G,
+                                  int chunk, int chunks, int S, int R,
+                                  float2* __restrict__ partial) {
+  extern __shared__ float2 red[];  // [R][C], reused as [C] per-channel (mean, M2)
   const int n = blockIdx.y, ch = blockIdx.x;
   const int tid = threadIdx.x;
   const int s = tid % S, r = tid / S;
@@ -85,13 +92,12 @@ __global__ void gn_partial_kernel(const f16* __restrict__ a, int Ca, int lda,
       s2[i] += d * d;
     }
   }
-  if (r < R) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) red[r * C + c + i] = make_float2(s1[i], s2[i]);
-  }
+  for (int i = 0; i < 8; ++i) red[r * C + c + i] = make_float2(s1[i], s2[i]);
   __syncthreads();
+  const float cnt = (float)(p1 - p0);
+  float2 mc[8];
   if (r == 0) {
-    const float cnt = (float)(p1 - p0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float t1 = 0.0f, t2 = 0.0f;
@@ -100,76 +106,90 @@ __global__ void gn_partial_kernel(const f16* __restrict__ a, int Ca, int lda,
         t1 += q.x;
         t2 += q.y;
       }
-      const float mean_d = t1 / cnt;
-      const float m2 = fmaxf(t2 - t1 * mean_d, 0.0f);
-      partial[((size_t)n * chunks + ch) * C + c + i] = make_float2(shift[i] + mean_d, m2);
+      const float md = t1 / cnt;
+      mc[i] = make_float2(shift[i] + md, fmaxf(t2 - t1 * md, 0.0f));
     }
+  }
+  __syncthreads();
+  if (r == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) red[c + i] = mc[i];
+  }
+  __syncthreads();
+  const int cpg = C / G;
+  for (int g = tid; g < G; g += blockDim.x) {
+    float mean = 0.0f;
+    for (int ci = 0; ci < cpg; ++ci) mean += red[g * cpg + ci].x;
+    mean /= (float)cpg;
+    float m2 = 0.0f;
+    for (int ci = 0; ci < cpg; ++ci) {
+      const float2 q = red[g * cpg + ci];
+      const float d = q.x - mean;
+      m2 += q.y + cnt * d * d;
+    }
+    partial[((size_t)n * chunks + ch) * G + g] = make_float2(mean, m2);
   }
 }
 
-// One block (64 threads) per (n, group): merge (chunk, channel) partials with
-// Chan's formula in fp64, then emit per-channel scale/shift.
+__device__ __forceinline__ void chan_merge(double& n, double& mean, double& m2, double nb,
+                                           double mb, double m2b) {
+  if (nb == 0.0) return;
+  const double tot = n + nb;
+  const double delta = mb - mean;
+  mean += delta * nb / tot;
+  m2 += m2b + delta * delta * n * nb / tot;
+  n = tot;
+}
+
+// One wave per (n, group): merge the chunk partials in fp64 (Chan), emit
+// per-channel scale = gamma*rstd and shift = beta - mean*scale.
 __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, int C, int G,
                                    int chunk, int chunks, const f16* __restrict__ gamma,
                                    const f16* __restrict__ beta, float eps,
                                    float2* __restrict__ ss) {
   const int n = blockIdx.x / G, g = blockIdx.x % G;
+  const int lane = threadIdx.x;
   const int cpg = C / G;
-  const int tid = threadIdx.x;
   double cnt = 0.0, mean = 0.0, m2 = 0.0;
-  const int entries = chunks * cpg;
-  for (int e = tid; e < entries; e += blockDim.x) {
-    const int chn = e / cpg, ci = e % cpg;
-    const float2 q = partial[((size_t)n * chunks + chn) * C + g * cpg + ci];
-    const double nb = (double)(min(HW, (chn + 1) * chunk) - chn * chunk);
-    const double delta = (double)q.x - mean;
-    const double tot = cnt + nb;
-    mean += delta * nb / tot;
-    m2 += (double)q.y + delta * delta * cnt * nb / tot;
-    cnt = tot;
+  for (int chn = lane; chn < chunks; chn += 64) {
+    const float2 q = partial[((size_t)n * chunks + chn) * G + g];
+    const double nb = (double)(min(HW, (chn + 1) * chunk) - chn * chunk) * cpg;
+    chan_merge(cnt, mean, m2, nb, (double)q.x, (double)q.y);
   }
-  __shared__ double sc[64], sm[64], sq[64];
-  sc[tid] = cnt;
-  sm[tid] = mean;
-  sq[tid] = m2;
-  __syncthreads();
-  if (tid == 0) {
-    double c0 = 0.0, mu = 0.0, q2 = 0.0;
-    for (int t = 0; t < (int)blockDim.x; ++t) {
-      const double nb = sc[t];
-      if (nb == 0.0) continue;
-      const double delta = sm[t] - mu;
-      const double tot = c0 + nb;
-      mu += delta * nb / tot;
-      q2 += sq[t] + delta * delta * c0 * nb / tot;
-      c0 = tot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double nb = __shfl_xor(cnt, o, 64);
+    const double mb = __shfl_xor(mean, o, 64);
+    const double qb = __shfl_xor(m2, o, 64);
+    // merge in a lane-order-independent way: lower lane id's data first
+    if ((lane & o) == 0) {
+      chan_merge(cnt, mean, m2, nb, mb, qb);
+    } else {
+      double n0 = nb, m0 = mb, q0 = qb;
+      chan_merge(n0, m0, q0, cnt, mean, m2);
+      cnt = n0; mean = m0; m2 = q0;
     }
-    sm[0] = mu;
-    sq[0] = q2 / c0;
   }
-  __syncthreads();
-  const double mu = sm[0];
-  const double var = sq[0] > 0.0 ? sq[0] : 0.0;
+  const double var = cnt > 0.0 ? fmax(m2 / cnt, 0.0) : 0.0;
   const float rstd = (float)(1.0 / sqrt(var + (double)eps));
-  for (int ci = tid; ci < cpg; ci += blockDim.x) {
+  for (int ci = lane; ci < cpg; ci += 64) {
     const int c = g * cpg + ci;
     const float gm = gamma ? (float)gamma[c] : 1.0f;
     const float bt = beta ? (float)beta[c] : 0.0f;
     const float scale = gm * rstd;
-    ss[(size_t)n * C + c] = make_float2(scale, bt - (float)mu * scale);
+    ss[(size_t)n * C + c] = make_float2(scale, bt - (float)mean * scale);
   }
 }
 
 __global__ void gn_apply_kernel(const f16* __restrict__ a, int Ca, int lda,
                                 const f16* __restrict__ b, int ldb, f16* __restrict__ out,
-                                int ldo, int HW, int C, long long total_vec,
+                                int ldo, int HW, int C, int total_vec,
                                 const float2* __restrict__ ss, int silu) {
   const int S = C / 8;
-  for (long long v = blockIdx.x * (long long)blockDim.x + threadIdx.x; v < total_vec;
-       v += (long long)gridDim.x * blockDim.x) {
-    const long long row = v / S;  // n*HW + p
-    const int s = (int)(v - row * S);
-    const int n = (int)(row / HW);
+  for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < total_vec; v += gridDim.x * blockDim.x) {
+    const int row = v / S;  // n*HW + p
+    const int s = v - row * S;
+    const int n = row / HW;
     const int c = s * 8;
     const f16* src = c < Ca ? a + (size_t)row * lda + c : b + (size_t)row * ldb + (c - Ca);
     float x[8];
@@ -197,7 +217,7 @@ int group_norm_nhwc(const void* in_a, int C_a, int ld_a, const void* in_b, int l
                     int C, int G, float eps, int silu, void* ws, hipStream_t s) {
   const GnPlan p = gn_plan(N, C, HW);
   float2* partial = (float2*)ws;
-  float2* ss = partial + (size_t)N * p.chunks * C;
+  float2* ss = partial + (size_t)N * p.chunks * G;
   ss = (float2*)(((uintptr_t)ss + 15) & ~(uintptr_t)15);
   const f16* a = (const f16*)in_a;
   const f16* b = in_b ? (const f16*)in_b : a;
@@ -205,15 +225,17 @@ int group_norm_nhwc(const void* in_a, int C_a, int ld_a, const void* in_b, int l
   if (red_bytes > 160 * 1024)
     return fail(DLM_ERR_UNSUPPORTED, "group_norm: channel count too large for one block");
   hipLaunchKernelGGL(gn_partial_kernel, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
-                     ld_a, b, ld_b, HW, C, p.chunk, p.chunks, p.S, p.R, partial);
+                     ld_a, b, ld_b, HW, C, G, p.chunk, p.chunks, p.S, p.R, partial);
   DLM_LAUNCH_CHECK();
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
                      p.chunks, (const f16*)gamma, (const f16*)beta, eps, ss);
   DLM_LAUNCH_CHECK();
   const long long total_vec = (long long)N * HW * (C / 8);
-  const int blocks = (int)std::min<long long>((total_vec + 255) / 256, 4096);
+  if (total_vec >= (1LL << 31) || (long long)N * HW * std::max(ld_a, ld_out) >= (1LL << 31))
+    return fail(DLM_ERR_UNSUPPORTED, "group_norm: tensor too large for 32-bit indexing");
+  const int blocks = (int)std::min<long long>((total_vec + 255) / 256, 8192);
   hipLaunchKernelGGL(gn_apply_kernel, dim3(blocks), dim3(256), 0, s, a, C_a, ld_a, b, ld_b,
-                     (f16*)out, ld_out, HW, C, total_vec, ss, silu);
+                     (f16*)out, ld_out, HW, C, (int)total_vec, ss, silu);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

@@ -82,6 +82,8 @@ extern "C" {
 
 const char* dlm_last_error(void) { return dlm::g_last_error.c_str(); }
 
+void dlm_set_last_error(const char* msg) { dlm::g_last_error = msg ? msg : ""; }
+
 int dlm_get_device_count(int* count) {
   DLM_REQUIRE(count != nullptr, "count is NULL");
   DLM_HIP(hipGetDeviceCount(count));

@@ -435,6 +435,6 @@ def sdxl_embed_inputs(timesteps: torch.Tensor, text_embeds: torch.Tensor, time_i
     _need(time_ids, 6 * (B if stride else 1), "time_ids")
     t_emb = torch.empty(B, 320, dtype=torch.float16, device=text_embeds.device)
     add_in = torch.empty(B, 2816, dtype=torch.float16, device=text_embeds.device)
-    call("dlm_sdxl_embed_inputs_fp16", _p(timesteps), _p(text_embeds), _p(time_ids), stride,
-         _p(t_emb), _p(add_in), B, stream_handle())
+    call("dlm_sdxl_embed_inputs_fp16", _p(timesteps), _p(text_embeds), 1280, _p(time_ids), stride,
+         256, _p(t_emb), 320, _p(add_in), B, stream_handle())
     return t_emb, add_in

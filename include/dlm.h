@@ -46,6 +46,9 @@ extern "C" {
 /* Replaces the CUDA_CHECK / std::runtime_error reporting of the reference
  * (src/kernels/utils.cuh:17-45): returns the last error text of this thread. */
 const char* dlm_last_error(void);
+/* Set this thread's error text (lets the C++ host layer report through the
+ * same channel). */
+void dlm_set_last_error(const char* msg);
 int dlm_get_device_count(int* count);
 int dlm_set_device(int device);
 /* Name of the GPU architecture of the current device (e.g. "gfx950"). */
@@ -227,11 +230,13 @@ int dlm_attention_strided_fp16(const dlm_attention_args* args, void* stream);
 
 /* SDXL conditioning inputs on the device (no host round trip, unlike the
  * reference's D2H of time_ids, src/infer/unet.cu:999-1000):
- * t_emb[b, 0:320] = sinusoid(timestep[b]) and
- * add_in[b, 0:2816] = text_embeds[b, 0:1280] ++ sinusoid_256(time_ids[b*ids_bstride + i]), i<6. */
-int dlm_sdxl_embed_inputs_fp16(const float* timesteps, const void* text_embeds,
-                               const void* time_ids, int ids_bstride, void* t_emb,
-                               void* add_in, int B, void* stream);
+ * t_emb[b, 0:t_dim] = sinusoid(timesteps[b]) and
+ * add_in[b] = text_embeds[b, 0:text_dim] ++ sinusoid_{id_dim}(time_ids[b*ids_bstride + i]), i < 6
+ * (SDXL: t_dim 320, text_dim 1280, id_dim 256, add_in width 2816; ids_bstride 0 shares
+ * one time_ids vector across the batch). */
+int dlm_sdxl_embed_inputs_fp16(const float* timesteps, const void* text_embeds, int text_dim,
+                               const void* time_ids, int ids_bstride, int id_dim, void* t_emb,
+                               int t_dim, void* add_in, int B, void* stream);
 
 /* Skinny linear for M <= 16 rows (the time / add embedding MLPs and the
  * per-resnet time_emb_proj): Y[m, n] = act(X'[m,:] . W[n,:] + bias[n]) where

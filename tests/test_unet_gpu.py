@@ -1,0 +1,148 @@
+"""Full UNet forward on the GPU against the fp32 CPU oracle.
+
+Gates: every stage within rel_err <= 1e-2 / cosine >= 0.9999, and noise_pred
+SSIM >= 0.99999 with the reference's SSIM (src/tests/test_unet.cu:161-201).
+Also: B=2 forward == two B=1 forwards bit for bit (reference
+test_diffusion_batch2 / test_conv2d B=2 == 2 x B=1), repeat forwards are
+bit-identical, and a warm forward performs no device allocation (the
+reference's arena contract, src/kernels/device_arena.cuh).
+"""
+import ctypes
+import math
+
+import pytest
+import torch
+
+from dollama_amd import unet as U
+from oracle import metrics
+from oracle import unet_ref as OR
+from tests._util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+TINY = U.UNetConfig(C0=64, C1=128, C2=192, depth1=1, depth2=2, cross_dim=96, text_dim=64, id_dim=16)
+assert OR.TINY.__dict__ == TINY.__dict__
+
+
+def _inputs(cfg, B, H, W, L, seed):
+    g = torch.Generator().manual_seed(seed)
+    lat = torch.randn(B, cfg.in_channels, H, W, generator=g)
+    ehs = torch.randn(B, L, cfg.cross_dim, generator=g)
+    text = torch.randn(B, cfg.text_dim, generator=g)
+    q = lambda t: t.half().float()
+    ids = torch.tensor([1024.0, 1024.0, 0.0, 0.0, 1024.0, 1024.0])
+    ts = torch.full((B,), 999.0)
+    return q(lat), ts, q(ehs), q(text), ids
+
+
+def _to_gpu(W):
+    return {k: v.half().cuda() for k, v in W.items()}
+
+
+def _run_gpu(cfg, Wg, lat, ts, ehs, text, ids, stages=None):
+    net = U.UNet(cfg)
+    net.set_weights(Wg)
+    net.prepare()
+    if stages is not None:
+        def hook(name, ptr, n, C):
+            buf = torch.empty(n, dtype=torch.float16, device="cuda:0")
+            torch.cuda.synchronize()
+            U._lib.call("dlm_memcpy", ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(ptr), n * 2, 2)
+            stages[name] = (buf.float().cpu(), C)
+        net.set_stage_hook(hook)
+    out = net.forward(lat.half().cuda(), ts.float().cuda(), ehs.half().cuda(), text.half().cuda(),
+                      ids.half().cuda())
+    torch.cuda.synchronize()
+    return net, out.float().cpu()
+
+
+def _nhwc_to_nchw(flat, C, like):
+    B, _, H, W = like.shape
+    return flat.reshape(B, H, W, C).permute(0, 3, 1, 2)
+
+
+def test_unet_tiny_parity_stages(gpu):
+    cfg = TINY
+    B, H, W, L = 2, 32, 32, 77
+    print(f"[case] tiny UNet B={B} {H}x{W} L={L}", flush=True)
+    Wc = OR.random_weights(OR.TINY, seed=7)
+    lat, ts, ehs, text, ids = _inputs(cfg, B, H, W, L, seed=8)
+    ref_st = {}
+    ref = OR.unet_forward(Wc, OR.TINY, lat, ts, ehs, text, ids, stages=ref_st)
+    st = {}
+    net, out = _run_gpu(cfg, _to_gpu(Wc), lat, ts, ehs, text, ids, stages=st)
+    for name in ["conv_in_out", "down_block_0_out", "down_block_1_out", "down_block_2_out",
+                 "mid_block_out", "up_block_0_out", "up_block_1_out", "up_block_2_out"]:
+        flat, C = st[name]
+        assert_close(_nhwc_to_nchw(flat, C, ref_st[name]), ref_st[name], f"tiny {name}")
+    assert_close(st["temb"][0].reshape(B, -1), ref_st["temb"], "tiny temb")
+    assert_close(out, ref, "tiny noise_pred")
+    s = metrics.ssim_uniform(out[:, :, :, :], ref)
+    print(f"[parity] tiny noise_pred SSIM={s:.7f}", flush=True)
+    assert s >= 0.99999
+    net.close()
+
+
+def test_unet_batch2_equals_two_batch1(gpu):
+    cfg = TINY
+    H = W = 32
+    print("[case] tiny UNet B=2 vs 2 x B=1", flush=True)
+    Wc = OR.random_weights(OR.TINY, seed=11)
+    lat, ts, ehs, text, ids = _inputs(cfg, 2, H, W, 77, seed=12)
+    net = U.UNet(cfg)
+    net.set_weights(_to_gpu(Wc))
+    net.prepare()
+    o2 = net.forward(lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
+    o2b = net.forward(lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
+    outs = []
+    for b in range(2):
+        outs.append(net.forward(lat[b:b + 1].half().cuda(), ts[b:b + 1].cuda(), ehs[b:b + 1].half().cuda(),
+                                text[b:b + 1].half().cuda(), ids.half().cuda()))
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o2b), "repeat forward not bit-identical"
+    assert torch.equal(o2, torch.cat(outs)), "B=2 differs from 2 x B=1"
+    net.close()
+
+
+def test_unet_warm_forward_no_device_alloc(gpu):
+    cfg = TINY
+    Wc = OR.random_weights(OR.TINY, seed=21)
+    lat, ts, ehs, text, ids = _inputs(cfg, 2, 32, 32, 77, seed=22)
+    net = U.UNet(cfg)
+    net.set_weights(_to_gpu(Wc))
+    net.prepare()
+    args = (lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
+    net.forward(*args)
+    torch.cuda.synchronize()
+    before = [U.arena_stats(a)["cuda_malloc_calls"] for a in (U.ARENA_UNET, U.ARENA_UNET_PERSIST)]
+    net.forward(*args)
+    torch.cuda.synchronize()
+    after = [U.arena_stats(a)["cuda_malloc_calls"] for a in (U.ARENA_UNET, U.ARENA_UNET_PERSIST)]
+    assert before == after, f"warm forward allocated device memory: {before} -> {after}"
+    assert U.arena_stats(U.ARENA_UNET_PERSIST)["live_request_bytes"] == 0
+    net.close()
+
+
+@pytest.mark.slow
+def test_unet_sdxl_full_parity(gpu):
+    """Full SDXL UNet, B=2 CFG, 1024x1024 image (latent 128x128), t=999."""
+    cfg = U.SDXL_CONFIG
+    B, H, W, L = 2, 128, 128, 77
+    print("[case] SDXL UNet B=2 128x128 vs fp32 CPU oracle", flush=True)
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    Wc = OR.random_weights(OR.SDXL, seed=1234)
+    lat, ts, ehs, text, ids = _inputs(cfg, B, H, W, L, seed=1235)
+    st = {}
+    net, out = _run_gpu(cfg, _to_gpu(Wc), lat, ts, ehs, text, ids, stages=st)
+    net.close()
+    torch.cuda.empty_cache()
+    ref_st = {}
+    ref = OR.unet_forward(Wc, OR.SDXL, lat, ts, ehs, text, ids, stages=ref_st)
+    for name in ["down_block_0_out", "down_block_1_out", "down_block_2_out", "mid_block_out",
+                 "up_block_0_out", "up_block_1_out", "up_block_2_out"]:
+        flat, C = st[name]
+        assert_close(_nhwc_to_nchw(flat, C, ref_st[name]), ref_st[name], f"sdxl {name}")
+    assert_close(out, ref, "sdxl noise_pred")
+    s = metrics.ssim_uniform(out, ref)
+    print(f"[parity] sdxl noise_pred SSIM={s:.7f}", flush=True)
+    assert s >= 0.99999
