@@ -104,6 +104,7 @@ HIP_SIGNATURES = {
     "dlm_linear_small_fp16": (I, [P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),
+    "dlm_gemm_force_tile": (I, [I]),
 }
 
 

@@ -49,29 +49,57 @@ struct EpiArgs {
 // ---------------------------------------------------------------------------
 // A/B operand loaders.  Each thread owns V 16-byte vectors of a 64-wide K
 // slice: vector i covers row (tid/8 + i*NT/8), halfs [8*(tid%8), +8).
+// Loads are raw buffer loads: a masked-off vector (tail row, tail K, zero
+// padding of the conv) gets an offset past the buffer end and reads zeros,
+// so the loaders have no branches and the compiler can keep several slices'
+// loads in flight with exact wait counts.
 // ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kOOB = (int)0x80000000;  // any offset >= the buffer size reads 0
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Branch-free choice between two wave-uniform values.  Written as
+// arithmetic: a select between two fields of one struct is otherwise turned
+// into an indexed load, which forces the struct into scratch memory.
+__device__ __forceinline__ int pick(bool c, int a, int b) { return b + (int)c * (a - b); }
+__device__ __forceinline__ unsigned pick(bool c, unsigned a, unsigned b) {
+  return b + (unsigned)c * (a - b);
+}
+__device__ __forceinline__ const f16* pick(bool c, const f16* a, const f16* b) {
+  const uint64_t ua = (uint64_t)a, ub = (uint64_t)b;
+  return (const f16*)(ub + (uint64_t)c * (ua - ub));
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(rsrc_t r, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+
 struct RowDesc {
   const f16* p;
   int ld;
   int rows;
   int K;
+  unsigned bytes;  // rows * ld * 2
 
   template <int BM, int NT>
   struct Loader {
     static constexpr int V = BM * BK / 8 / NT;
-    const f16* p;
+    rsrc_t rs;
     int ld, rows, K, row0, cv;
     __device__ Loader(const RowDesc& d, int r0, int tid)
-        : p(d.p), ld(d.ld), rows(d.rows), K(d.K), row0(r0 + tid / 8), cv(tid % 8) {}
+        : rs(make_rsrc(d.p, d.bytes)), ld(d.ld), rows(d.rows), K(d.K), row0(r0 + tid / 8),
+          cv(tid % 8) {}
     __device__ __forceinline__ void load(int kt, u32x4 (&r)[V]) const {
       const int k = kt * BK + cv * 8;
+      const bool kin = k < K;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const int row = row0 + i * (NT / 8);
-        if (row < rows && k < K)
-          r[i] = *reinterpret_cast<const u32x4*>(p + (size_t)row * ld + k);
-        else
-          r[i] = u32x4{0u, 0u, 0u, 0u};
+        const int off = (row < rows && kin) ? (row * ld + k) * 2 : kOOB;
+        r[i] = buffer_load16(rs, off);
       }
     }
   };
@@ -91,7 +119,8 @@ struct ConvParams {
   const f16* s1b;
   int C1a, C1, ld1a, ld1b;
   int HoWo, Wo, M;
-  int generic;  // 1 when C0 is not a multiple of 64 (per-vector tap decode)
+  int generic;  // 1 when C0 is not a multiple of 64 (per-vector tap decode, no concat)
+  unsigned bytes0a, bytes0b, bytes1a, bytes1b;
 };
 
 struct ConvDesc : ConvParams {
@@ -124,71 +153,62 @@ struct ConvDesc : ConvParams {
     }
     __device__ __forceinline__ void load(int kt, u32x4 (&r)[V]) const {
       const int k0 = kt * BK;
+      int off[V];
+      rsrc_t rs;
       if (k0 < d.K0) {
+        int kh, kw, ld, cc;
+        bool kin = true;
         if (!d.generic) {
-          // one tap per K slice (C0 % 64 == 0): tap / channel are wave-uniform
+          // one tap per K slice (C0 % 64 == 0): tap and channel are wave-uniform
           const int tap = k0 / d.C0;
           const int c = k0 - tap * d.C0;
-          const int kh = tap / d.KW;
-          const int kw = tap - kh * d.KW;
-          const f16* src;
-          int ld, cc;
-          if (c < d.C0a) {
-            src = d.s0a; ld = d.ld0a; cc = c;
-          } else {
-            src = d.s0b; ld = d.ld0b; cc = c - d.C0a;
-          }
-          src += cc + cv * 8;
-#pragma unroll
-          for (int i = 0; i < V; ++i) {
-            int ih = ihb[i] + kh, iw = iwb[i] + kw;
-            const bool ok = pbase[i] >= 0 && (unsigned)ih < (unsigned)d.Hv &&
-                            (unsigned)iw < (unsigned)d.Wv;
-            if (d.up) { ih >>= 1; iw >>= 1; }
-            if (ok)
-              r[i] = *reinterpret_cast<const u32x4*>(src + (size_t)(pbase[i] + ih * d.W + iw) * ld);
-            else
-              r[i] = u32x4{0u, 0u, 0u, 0u};
-          }
+          kh = tap / d.KW;
+          kw = tap - kh * d.KW;
+          const bool isa = c < d.C0a;
+          // select pointer and size, then build the descriptor (a select on
+          // descriptor values is lowered through scratch memory)
+          rs = make_rsrc(pick(isa, d.s0a, d.s0b), pick(isa, d.bytes0a, d.bytes0b));
+          ld = pick(isa, d.ld0a, d.ld0b);
+          cc = pick(isa, c, c - d.C0a) + cv * 8;
         } else {
           // small-channel convs (conv_in): decode the tap per 8-channel vector
           const int k = k0 + cv * 8;
-          const bool kin = k < d.K0;
+          kin = k < d.K0;
           const int tap = kin ? k / d.C0 : 0;
-          const int c = k - tap * d.C0;
-          const int kh = tap / d.KW;
-          const int kw = tap - kh * d.KW;
-          const bool isa = c < d.C0a;
-          const f16* src = isa ? d.s0a + c : d.s0b + (c - d.C0a);
-          const int ld = isa ? d.ld0a : d.ld0b;
+          cc = k - tap * d.C0;
+          kh = tap / d.KW;
+          kw = tap - kh * d.KW;
+          rs = make_rsrc(d.s0a, d.bytes0a);
+          ld = d.ld0a;
+        }
 #pragma unroll
-          for (int i = 0; i < V; ++i) {
-            int ih = ihb[i] + kh, iw = iwb[i] + kw;
-            const bool ok = kin && pbase[i] >= 0 && (unsigned)ih < (unsigned)d.Hv &&
-                            (unsigned)iw < (unsigned)d.Wv;
-            if (d.up) { ih >>= 1; iw >>= 1; }
-            if (ok)
-              r[i] = *reinterpret_cast<const u32x4*>(src + (size_t)(pbase[i] + ih * d.W + iw) * ld);
-            else
-              r[i] = u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < V; ++i) {
+          int ih = ihb[i] + kh, iw = iwb[i] + kw;
+          const bool ok = kin && pbase[i] >= 0 && (unsigned)ih < (unsigned)d.Hv &&
+                          (unsigned)iw < (unsigned)d.Wv;
+          if (d.up) {
+            ih >>= 1;
+            iw >>= 1;
           }
+          off[i] = ok ? ((pbase[i] + ih * d.W + iw) * ld + cc) * 2 : kOOB;
         }
       } else {
-        // segment 1 (1x1 over the block input at output resolution)
-        const int c = k0 - d.K0 + cv * 8;
-        const bool cin = c < d.C1;
-        const bool isa = c < d.C1a;
-        const f16* src = isa ? d.s1a + c : d.s1b + (c - d.C1a);
-        const int ld = isa ? d.ld1a : d.ld1b;
+        // segment 1 (1x1 over the block input at output resolution); the
+        // a/b split is 64-aligned so the source is wave-uniform
+        const int cs = k0 - d.K0;
+        const bool isa = cs < d.C1a;
+        rs = make_rsrc(pick(isa, d.s1a, d.s1b), pick(isa, d.bytes1a, d.bytes1b));
+        const int ld = pick(isa, d.ld1a, d.ld1b);
+        const int c = pick(isa, cs, cs - d.C1a) + cv * 8;
+        const bool cin = cs + cv * 8 < d.C1;
 #pragma unroll
         for (int i = 0; i < V; ++i) {
           const int m = row0 + i * (NT / 8);
-          if (cin && m < d.M)
-            r[i] = *reinterpret_cast<const u32x4*>(src + (size_t)m * ld);
-          else
-            r[i] = u32x4{0u, 0u, 0u, 0u};
+          off[i] = (cin && m < d.M) ? (m * ld + c) * 2 : kOOB;
         }
       }
+#pragma unroll
+      for (int i = 0; i < V; ++i) r[i] = buffer_load16(rs, off[i]);
     }
   };
 };
@@ -214,6 +234,53 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tn = rem / gsz;
 }
 
+// Epilogue of one 32x32 accumulator block: lane owns column `col`, element
+// e is row row0 + mfma_row(e, lane).  Kept as a separate inlined function
+// whose 16-element loop always unrolls, so the accumulators stay in registers.
+__device__ __forceinline__ void epilogue_tile(const f32x16& a, int row0, int col, int lane,
+                                              const EpiArgs& ep) {
+  const bool col_ok = col < ep.N;
+  const float bcol = (ep.bias && col_ok) ? (float)ep.bias[col] : 0.0f;
+  if (ep.act == DLM_ACT_GEGLU) {
+    // columns are interleaved in blocks of 16: lanes with (lane & 16) == 0
+    // hold the value column, their xor-16 partner the matching gate column
+    const bool is_val = (lane & 16) == 0;
+    const int ocol = (col >> 5) * 16 + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float h = a[e] * ep.alpha + bcol;
+      const float g = __shfl_xor(h, 16, 64);
+      const int row = row0 + mfma_row(e, lane);
+      if (is_val && col_ok && row < ep.M) {
+        float v = h * gelu_erf_f(g);
+        if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol];
+        ep.y[(size_t)row * ep.ldy + ocol] = (f16)v;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = row0 + mfma_row(e, lane);
+    if (col_ok && row < ep.M) {
+      float v = a[e] * ep.alpha + bcol;
+      int n = 0, p = row;
+      if (ep.rows_per_sample > 0) {
+        n = row / ep.rows_per_sample;
+        p = row - n * ep.rows_per_sample;
+      }
+      if (ep.tbias) v += (float)ep.tbias[(size_t)n * ep.tbias_ld + col];
+      if (ep.act == DLM_ACT_SILU) v = silu_f(v);
+      else if (ep.act == DLM_ACT_GELU) v = gelu_erf_f(v);
+      if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + col];
+      if (ep.out_nchw)
+        ep.y[((size_t)n * ep.N + col) * ep.rows_per_sample + p] = (f16)v;
+      else
+        ep.y[(size_t)row * ep.ldy + col] = (f16)v;
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, class Desc>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
@@ -223,6 +290,8 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
   constexpr int AV = BM * BK / 8 / NT;
   constexpr int BV = BN * BK / 8 / NT;
   static_assert(AV * NT * 8 == BM * BK && BV * NT * 8 == BN * BK, "tile/thread mismatch");
+  // two slices in flight for small wave tiles, one for >= 8 MFMA blocks per wave
+  constexpr bool kDeep = TM * TN < 8;
   constexpr int STAGE = (BM + BN) * LS;
   __shared__ __attribute__((aligned(16))) f16 smem[2 * STAGE];
 
@@ -238,13 +307,17 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
   RowDesc::Loader<BN, NT> bl(bd, n0, tid);
   const int K = bd.K;
   const int nk = (K + BK - 1) / BK;
+  const int last = nk - 1;
 
-  u32x4 ra[AV], rb[BV];
-  al.load(0, ra);
-  bl.load(0, rb);
-  {
-    f16* As = smem;
-    f16* Bs = smem + BM * LS;
+  // Pipeline: LDS holds slice kt (double-buffered); two register sets hold
+  // slices kt+1 and kt+2 in flight, so each global load has two slices of
+  // MFMA work to land.  Loads past the end re-read the last slice (clamped)
+  // so every load and wait count stays unconditional.
+  u32x4 ra0[AV], rb0[BV];
+  u32x4 ra1[kDeep ? AV : 1], rb1[kDeep ? BV : 1];
+  auto stage_lds = [&](int buf, const u32x4(&ra)[AV], const u32x4(&rb)[BV]) {
+    f16* As = smem + buf * STAGE;
+    f16* Bs = As + BM * LS;
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
       const int v = tid + i * NT;
@@ -255,8 +328,7 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
       const int v = tid + i * NT;
       *reinterpret_cast<u32x4*>(Bs + (v >> 3) * LS + (v & 7) * 8) = rb[i];
     }
-  }
-  __syncthreads();
+  };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -269,98 +341,121 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
   const int a_row = wm * WM + (lane & 31);
   const int b_row = wn * WN + (lane & 31);
   const int k_off = (lane >> 5) * 8;
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      al.load(kt + 1, ra);
-      bl.load(kt + 1, rb);
-    }
-    const f16* As = smem + cur * STAGE;
+  // Fragment registers are double-buffered across the four 16-wide k-steps of
+  // a slice: the ds_reads of step s+1 are issued before the MFMAs of step s,
+  // and the staging of the next slice into the other LDS buffer is spread
+  // over the first two steps, so LDS traffic overlaps the MFMA pipe instead
+  // of alternating with it.
+  f16x8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  auto rd = [&](int buf, int ks, f16x8 (&fa)[TM], f16x8 (&fb)[TN]) {
+    const f16* As = smem + buf * STAGE;
     const f16* Bs = As + BM * LS;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      f16x8 af[TM], bf[TN];
+    for (int i = 0; i < TM; ++i)
+      fa[i] = *reinterpret_cast<const f16x8*>(As + (a_row + i * 32) * LS + ks * 16 + k_off);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const f16x8*>(As + (a_row + i * 32) * LS + ks * 16 + k_off);
+    for (int j = 0; j < TN; ++j)
+      fb[j] = *reinterpret_cast<const f16x8*>(Bs + (b_row + j * 32) * LS + ks * 16 + k_off);
+  };
+  auto mm = [&](const f16x8 (&fa)[TM], const f16x8 (&fb)[TN]) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const f16x8*>(Bs + (b_row + j * 32) * LS + ks * 16 + k_off);
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fa[i], fb[j], acc[i][j]);
+  };
+  // write half `part` of the staged registers into LDS buffer `buf`
+  auto stage_half = [&](int buf, const u32x4(&ra)[AV], const u32x4(&rb)[BV], int part) {
+    f16* As = smem + buf * STAGE;
+    f16* Bs = As + BM * LS;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
-    }
-    if (more) {
-      f16* An = smem + (cur ^ 1) * STAGE;
-      f16* Bn = An + BM * LS;
-#pragma unroll
-      for (int i = 0; i < AV; ++i) {
+    for (int i = 0; i < AV; ++i) {
+      if ((i * 2 < AV) == (part == 0)) {
         const int v = tid + i * NT;
-        *reinterpret_cast<u32x4*>(An + (v >> 3) * LS + (v & 7) * 8) = ra[i];
-      }
-#pragma unroll
-      for (int i = 0; i < BV; ++i) {
-        const int v = tid + i * NT;
-        *reinterpret_cast<u32x4*>(Bn + (v >> 3) * LS + (v & 7) * 8) = rb[i];
+        *reinterpret_cast<u32x4*>(As + (v >> 3) * LS + (v & 7) * 8) = ra[i];
       }
     }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      if ((i * 2 < BV) == (part == 0)) {
+        const int v = tid + i * NT;
+        *reinterpret_cast<u32x4*>(Bs + (v >> 3) * LS + (v & 7) * 8) = rb[i];
+      }
+    }
+  };
+  // one K slice from LDS buffer `buf` (step-0 fragments already in fa0/fb0),
+  // staging ra/rb into buffer `nbuf`; leaves step 0 of nothing in flight
+  auto slice = [&](int buf, int nbuf, const u32x4(&ra)[AV], const u32x4(&rb)[BV], bool stage) {
+    rd(buf, 1, fa1, fb1);
+    mm(fa0, fb0);
+    if (stage) stage_half(nbuf, ra, rb, 0);
+    rd(buf, 2, fa0, fb0);
+    mm(fa1, fb1);
+    if (stage) stage_half(nbuf, ra, rb, 1);
+    rd(buf, 3, fa1, fb1);
+    mm(fa0, fb0);
+    mm(fa1, fb1);
+  };
+
+  al.load(0, ra0);
+  bl.load(0, rb0);
+  stage_lds(0, ra0, rb0);
+  if constexpr (!kDeep) {
+    // one slice in flight: enough when a slice carries >= 32 MFMAs per wave
+    al.load(min(1, last), ra0);
+    bl.load(min(1, last), rb0);
     __syncthreads();
+    rd(0, 0, fa0, fb0);
+    int kt = 0;
+    for (; kt < last; ++kt) {
+      const int cur = kt & 1;
+      slice(cur, cur ^ 1, ra0, rb0, true);
+      __syncthreads();
+      rd(cur ^ 1, 0, fa0, fb0);
+      al.load(min(kt + 2, last), ra0);
+      bl.load(min(kt + 2, last), rb0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    slice(kt & 1, 0, ra0, rb0, false);
+  } else {
+  al.load(min(1, last), ra1);
+  bl.load(min(1, last), rb1);
+  al.load(min(2, last), ra0);
+  bl.load(min(2, last), rb0);
+  __syncthreads();
+  rd(0, 0, fa0, fb0);
+
+  // Slices are consumed in pairs by a loop with a single exit (a second exit
+  // sharing the latch makes the wait-count analysis treat the newer register
+  // set as the older one and drain every load); sched_barrier keeps each
+  // load group where it is written instead of letting it sink below the
+  // LDS stores of the other set.
+  int kt = 0;
+  for (; kt + 1 <= last; kt += 2) {
+    // even slice: LDS buffer 0 holds kt, ra1 holds kt+1, ra0 holds kt+2
+    slice(0, 1, ra1, rb1, true);
+    __syncthreads();
+    rd(1, 0, fa0, fb0);
+    al.load(min(kt + 3, last), ra1);
+    bl.load(min(kt + 3, last), rb1);
+    __builtin_amdgcn_sched_barrier(0);
+    // odd slice: LDS buffer 1 holds kt+1, ra0 holds kt+2, ra1 holds kt+3
+    slice(1, 0, ra0, rb0, true);
+    __syncthreads();
+    rd(0, 0, fa0, fb0);
+    al.load(min(kt + 4, last), ra0);
+    bl.load(min(kt + 4, last), rb0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (kt == last) slice(0, 1, ra1, rb1, false);  // odd slice count: buffer 0 holds the last slice
   }
 
   // ------------------------------ epilogue ------------------------------
   const int row_base = m0 + wm * WM;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int col = n0 + wn * WN + j * 32 + (lane & 31);
-    const bool col_ok = col < ep.N;
-    const float bcol = (ep.bias && col_ok) ? (float)ep.bias[col] : 0.0f;
-    if (ep.act == DLM_ACT_GEGLU) {
-      // columns are interleaved in blocks of 16: lanes with (lane & 16) == 0
-      // hold the value column, their xor-16 partner the matching gate column
-      const bool is_val = (lane & 16) == 0;
-      const int ocol = (col >> 5) * 16 + (lane & 15);
+  for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float h = acc[i][j][e] * ep.alpha + bcol;
-          const float g = __shfl_xor(h, 16, 64);
-          const int row = row_base + i * 32 + mfma_row(e, lane);
-          if (is_val && col_ok && row < ep.M) {
-            float v = h * gelu_erf_f(g);
-            if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol];
-            ep.y[(size_t)row * ep.ldy + ocol] = (f16)v;
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = row_base + i * 32 + mfma_row(e, lane);
-          if (!col_ok || row >= ep.M) continue;
-          float v = acc[i][j][e] * ep.alpha + bcol;
-          int n = 0, p = row;
-          if (ep.rows_per_sample > 0) {
-            n = row / ep.rows_per_sample;
-            p = row - n * ep.rows_per_sample;
-          }
-          if (ep.tbias) v += (float)ep.tbias[(size_t)n * ep.tbias_ld + col];
-          if (ep.act == DLM_ACT_SILU) v = silu_f(v);
-          else if (ep.act == DLM_ACT_GELU) v = gelu_erf_f(v);
-          if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + col];
-          if (ep.out_nchw)
-            ep.y[((size_t)n * ep.N + col) * ep.rows_per_sample + p] = (f16)v;
-          else
-            ep.y[(size_t)row * ep.ldy + col] = (f16)v;
-        }
-      }
-    }
-  }
+    for (int i = 0; i < TM; ++i)
+      epilogue_tile(acc[i][j], row_base + i * 32, n0 + wn * WN + j * 32 + (lane & 31), lane, ep);
 }
 
 // ---------------------------------------------------------------------------
@@ -380,10 +475,22 @@ static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
 
 static inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 
+// Tile-shape override for tuning sweeps (0 = automatic choice).
+static int g_forced_tile = 0;
+
 template <class Desc>
 static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                        hipStream_t s) {
   constexpr int kCUs = 256;
+  switch (g_forced_tile) {
+    case 1: return launch_cfg<128, 128, 64, 64>(ad, bd, ep, M, N, s);
+    case 2: return launch_cfg<128, 64, 64, 32>(ad, bd, ep, M, N, s);
+    case 3: return launch_cfg<64, 64, 32, 32>(ad, bd, ep, M, N, s);
+    case 4: return launch_cfg<128, 32, 32, 32>(ad, bd, ep, M, N, s);
+    case 5: return launch_cfg<256, 128, 128, 64>(ad, bd, ep, M, N, s);
+    case 6: return launch_cfg<128, 256, 64, 128>(ad, bd, ep, M, N, s);
+    default: break;
+  }
   if (N <= 32) return launch_cfg<128, 32, 32, 32>(ad, bd, ep, M, N, s);
   if (N <= 64) return launch_cfg<128, 64, 64, 32>(ad, bd, ep, M, N, s);
   if (ceil_div(M, 128) * ceil_div(N, 128) >= kCUs)
@@ -416,8 +523,8 @@ static EpiArgs make_epi(void* Y, int ldy, const void* bias, const void* R, int l
 int linear_impl(const void* X, int lda, const void* W, int ldw, const void* bias, const void* R,
                 int ldr, void* Y, int ldy, int M, int N, int K, float alpha, float beta, int act,
                 hipStream_t s) {
-  RowDesc ad{(const f16*)X, lda, M, K};
-  RowDesc bd{(const f16*)W, ldw, N, K};
+  RowDesc ad{(const f16*)X, lda, M, K, (unsigned)((size_t)M * lda * 2)};
+  RowDesc bd{(const f16*)W, ldw, N, K, (unsigned)((size_t)N * ldw * 2)};
   EpiArgs ep = make_epi(Y, ldy, bias, R, ldr, M, N, alpha, beta, act);
   return launch_gemm(ad, bd, ep, M, N, s);
 }
@@ -571,8 +678,13 @@ int conv_nhwc_impl(const dlm_conv_nhwc_args* a, hipStream_t s) {
   d.Wo = Wo;
   d.M = a->N * Ho * Wo;
   d.generic = (C0 % BK != 0 || a->C0a % BK != 0) ? 1 : 0;
+  const size_t in_pix = (size_t)a->N * a->H * a->W;
+  d.bytes0a = (unsigned)(in_pix * a->ld0a * 2);
+  d.bytes0b = (unsigned)(in_pix * a->ld0b * 2);
+  d.bytes1a = (unsigned)((size_t)d.M * a->ld1a * 2);
+  d.bytes1b = (unsigned)((size_t)d.M * a->ld1b * 2);
   const int K = d.K0 + C1;
-  RowDesc bd{(const f16*)a->weight, a->ldw, a->Cout, K};
+  RowDesc bd{(const f16*)a->weight, a->ldw, a->Cout, K, (unsigned)((size_t)a->Cout * a->ldw * 2)};
   EpiArgs ep = make_epi(a->out, a->ldy, a->bias, a->residual, a->res_ld, d.M, a->Cout, 1.0f, 1.0f,
                         a->act);
   ep.tbias = (const f16*)a->tbias;
@@ -599,6 +711,8 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
   DLM_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K, lda and ldw must be multiples of 8");
   DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
   DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
+  DLM_REQUIRE(2LL * M * lda < (1LL << 31) && 2LL * N * ldw < (1LL << 31),
+              "X or W larger than 2 GiB");
   DLM_REQUIRE(act >= DLM_ACT_NONE && act <= DLM_ACT_GELU, "unknown act");
   if (act == DLM_ACT_GEGLU) {
     DLM_REQUIRE(N % 32 == 0, "GEGLU needs N (interleaved value+gate columns) % 32 == 0");
@@ -733,9 +847,16 @@ int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* a, void* stream) {
   DLM_REQUIRE(!a->tbias || a->tbias_ld >= a->Cout, "tbias_ld < Cout");
   DLM_REQUIRE(a->act == DLM_ACT_NONE || a->act == DLM_ACT_SILU || a->act == DLM_ACT_GELU,
               "conv act must be none/silu/gelu");
-  DLM_REQUIRE((long long)a->N * Hv * Wv * std::max(a->ld0a, a->ld0b) < (1LL << 31) &&
-                  (long long)a->N * Ho * Wo < (1LL << 31),
-              "tensor too large for 32-bit pixel indexing");
+  // every operand is addressed through a buffer resource with 32-bit byte
+  // offsets; masked vectors use offset 2^31, so each operand stays below that
+  const long long in_pix = (long long)a->N * a->H * a->W;
+  const long long out_pix = (long long)a->N * Ho * Wo;
+  DLM_REQUIRE(2 * in_pix * std::max(a->ld0a, a->ld0b) < (1LL << 31) &&
+                  2 * out_pix * std::max(a->ld1a, a->ld1b) < (1LL << 31) &&
+                  2LL * a->Cout * a->ldw < (1LL << 31),
+              "operand larger than 2 GiB");
+  DLM_REQUIRE((C0 % BK == 0 && a->C0a % BK == 0) || a->C0b == 0,
+              "channel concatenation needs 64-aligned channel counts");
   return conv_nhwc_impl(a, (hipStream_t)stream);
 }
 
@@ -789,3 +910,9 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
 }
 
 }  // extern "C"
+
+extern "C" int dlm_gemm_force_tile(int tile_id) {
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 6, "tile_id must be in [0, 6]");
+  dlm::g_forced_tile = tile_id;
+  return DLM_OK;
+}

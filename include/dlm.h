@@ -140,6 +140,11 @@ int dlm_conv_bias_residual_fp16(const void* conv, const void* convbias, const vo
 int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_period,
                                 void* stream);
 
+/* Tuning aid: force the MFMA GEMM / conv tile shape for every following
+ * launch in this process (0 = automatic; 1 = 128x128, 2 = 128x64,
+ * 3 = 64x64, 4 = 128x32, 5 = 256x128, 6 = 128x256 output tiles). */
+int dlm_gemm_force_tile(int tile_id);
+
 /* ------------------------------------------------------------------ */
 /* Channels-last fused entry points (native forms used by the UNet)     */
 /* ------------------------------------------------------------------ */
