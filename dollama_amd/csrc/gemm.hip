@@ -281,7 +281,7 @@ __device__ __forceinline__ void epilogue_tile(const f32x16& a, int row0, int col
   }
 }
 
-template <int BM, int BN, int WM, int WN, class Desc>
+template <int BM, int BN, int WM, int WN, bool DEEP, class Desc>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
   constexpr int WAVES_N = BN / WN;
@@ -290,8 +290,8 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
   constexpr int AV = BM * BK / 8 / NT;
   constexpr int BV = BN * BK / 8 / NT;
   static_assert(AV * NT * 8 == BM * BK && BV * NT * 8 == BN * BK, "tile/thread mismatch");
-  // two slices in flight for small wave tiles, one for >= 8 MFMA blocks per wave
-  constexpr bool kDeep = TM * TN < 8;
+  // DEEP: two slices in flight in registers (one otherwise)
+  constexpr bool kDeep = DEEP;
   constexpr int STAGE = (BM + BN) * LS;
   __shared__ __attribute__((aligned(16))) f16 smem[2 * STAGE];
 
@@ -461,14 +461,14 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
 // ---------------------------------------------------------------------------
 // Host-side tile configuration choice and launch.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int WM, int WN, class Desc>
+template <int BM, int BN, int WM, int WN, bool DEEP = true, class Desc>
 static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                       hipStream_t s) {
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
-  hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, WM, WN, Desc>), dim3(tiles_m * tiles_n), dim3(NT),
-                     0, s, ad, bd, ep, tiles_m, tiles_n);
+  hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, WM, WN, DEEP, Desc>), dim3(tiles_m * tiles_n),
+                     dim3(NT), 0, s, ad, bd, ep, tiles_m, tiles_n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -489,6 +489,7 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
     case 4: return launch_cfg<128, 32, 32, 32>(ad, bd, ep, M, N, s);
     case 5: return launch_cfg<256, 128, 128, 64>(ad, bd, ep, M, N, s);
     case 6: return launch_cfg<128, 256, 64, 128>(ad, bd, ep, M, N, s);
+    case 7: return launch_cfg<256, 256, 128, 128>(ad, bd, ep, M, N, s);
     default: break;
   }
   if (N <= 32) return launch_cfg<128, 32, 32, 32>(ad, bd, ep, M, N, s);
@@ -912,7 +913,7 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
 }  // extern "C"
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 6, "tile_id must be in [0, 6]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 7, "tile_id must be in [0, 7]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

@@ -142,7 +142,8 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
 
 /* Tuning aid: force the MFMA GEMM / conv tile shape for every following
  * launch in this process (0 = automatic; 1 = 128x128, 2 = 128x64,
- * 3 = 64x64, 4 = 128x32, 5 = 256x128, 6 = 128x256 output tiles). */
+ * 3 = 64x64, 4 = 128x32, 5 = 256x128, 6 = 128x256, 7 = 256x256 output
+ * tiles). */
 int dlm_gemm_force_tile(int tile_id);
 
 /* ------------------------------------------------------------------ */

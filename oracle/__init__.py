@@ -11,8 +11,10 @@ Contents
                references (independent of torch); built to libnaive.so
   naive.py     ctypes binding of libnaive.so
   unet_ref.py  fp32 torch-CPU restatement of the SDXL UNet graph
-  scheduler.py Euler discrete scheduler (scaled_linear, leading spacing)
   metrics.py   tolerance metrics: relative error, cosine, the reference SSIM
+  sched_ref.cpp  driver of the reference's own header-only Euler scheduler
+               (src/infer/scheduler.hpp), compiled by the Makefile from the
+               reference tree into _ref/sched_ref when that tree is present
 
 How each function is pinned (besides these two independent restatements
 agreeing with each other) is listed in tests/test_oracle.py.
