@@ -241,24 +241,6 @@ __device__ __forceinline__ void epilogue_tile(const f32x16& a, int row0, int col
                                               const EpiArgs& ep) {
   const bool col_ok = col < ep.N;
   const float bcol = (ep.bias && col_ok) ? (float)ep.bias[col] : 0.0f;
-  if (ep.act == DLM_ACT_GEGLU) {
-    // columns are interleaved in blocks of 16: lanes with (lane & 16) == 0
-    // hold the value column, their xor-16 partner the matching gate column
-    const bool is_val = (lane & 16) == 0;
-    const int ocol = (col >> 5) * 16 + (lane & 15);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float h = a[e] * ep.alpha + bcol;
-      const float g = __shfl_xor(h, 16, 64);
-      const int row = row0 + mfma_row(e, lane);
-      if (is_val && col_ok && row < ep.M) {
-        float v = h * gelu_erf_f(g);
-        if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol];
-        ep.y[(size_t)row * ep.ldy + ocol] = (f16)v;
-      }
-    }
-    return;
-  }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int row = row0 + mfma_row(e, lane);
@@ -277,6 +259,27 @@ __device__ __forceinline__ void epilogue_tile(const f32x16& a, int row0, int col
         ep.y[((size_t)n * ep.N + col) * ep.rows_per_sample + p] = (f16)v;
       else
         ep.y[(size_t)row * ep.ldy + col] = (f16)v;
+    }
+  }
+}
+
+// GEGLU epilogue of a (value, gate) pair of 32x32 blocks: the packed weight
+// puts value rows 32p..32p+31 and the matching gate rows in adjacent 32-row
+// blocks, so both halves of an output element sit in the same lane and
+// register.  `ocol` is the output column of this lane.
+__device__ __forceinline__ void epilogue_geglu_tile(const f32x16& av, const f32x16& ag, int row0,
+                                                    int col, int ocol, int lane,
+                                                    const EpiArgs& ep) {
+  if (col >= ep.N) return;
+  const float bv = ep.bias ? (float)ep.bias[col] : 0.0f;
+  const float bg = ep.bias ? (float)ep.bias[col + 32] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = row0 + mfma_row(e, lane);
+    if (row < ep.M) {
+      float v = (av[e] * ep.alpha + bv) * gelu_erf_f(ag[e] * ep.alpha + bg);
+      if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol];
+      ep.y[(size_t)row * ep.ldy + ocol] = (f16)v;
     }
   }
 }
@@ -451,6 +454,19 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
 
   // ------------------------------ epilogue ------------------------------
   const int row_base = m0 + wm * WM;
+  if constexpr (TN % 2 == 0) {
+    if (ep.act == DLM_ACT_GEGLU) {
+#pragma unroll
+      for (int j = 0; j < TN; j += 2)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int col = n0 + wn * WN + j * 32 + (lane & 31);
+          const int ocol = (n0 + wn * WN) / 2 + (j / 2) * 32 + (lane & 31);
+          epilogue_geglu_tile(acc[i][j], acc[i][j + 1], row_base + i * 32, col, ocol, lane, ep);
+        }
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -458,9 +474,372 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
       epilogue_tile(acc[i][j], row_base + i * 32, n0 + wn * WN + j * 32 + (lane & 31), lane, ep);
 }
 
+// ===========================================================================
+// LDS-DMA GEMM core.  Used for every linear whose operands and output are
+// suitably aligned and for convolutions whose channel counts are multiples of
+// 64 (all of the UNet except conv_in); the kernel above remains the general
+// fallback.
+//
+// Operand staging: global -> LDS directly (buffer_load ... lds), no VGPR
+// staging and no ds_write; on gfx950 ds_write_b128 moves ~72 B/clk/CU, half
+// of what a tile needs, while the direct path leaves the LDS write port to
+// the DMA.  Each 64-wide K slice of a row is 128 contiguous bytes, so every
+// L2 request is a full line.  LDS rows are 128 B (no padding) with the
+// 16-byte chunks XOR-swizzled by (row >> 1) & 7: the 16 rows one ds_read_b128
+// phase touches then cover all 64 banks exactly once.
+//
+// Pipeline: an NS-slice ring in LDS; slice kt+NS-1 is requested while slice
+// kt is consumed; one s_waitcnt vmcnt + s_barrier per slice.  Fragment reads
+// of k-step s+1 are issued before the MFMAs of step s.
+//
+// MFMA form: acc = W-fragment x X-fragment, i.e. the transposed product, so a
+// lane holds one output row and, per group q, four consecutive output
+// columns: the epilogue stores 8 bytes per instruction and reads bias and
+// residual as 8-byte vectors.
+// ===========================================================================
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define DLM_LDS __attribute__((address_space(3)))
+
+// 128-bit raw-buffer descriptor in SGPRs: base, no stride, byte size
+// (offsets at or past it read 0).
+__device__ __forceinline__ i32x4 dma_rsrc(const void* p, unsigned bytes) {
+  const uint64_t a = (uint64_t)p;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// One wave-wide global -> LDS copy: lane l reads 16 bytes at byte offset voff
+// of the buffer and the hardware writes them to LDS at dst + 16 l (dst goes
+// through M0).  Issued as inline asm so the compiler neither tracks nor
+// drains it: the kernel orders it with explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const i32x4& r, const unsigned char DLM_LDS* dst, int voff) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
+               "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding: vmcnt in bits
+// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+#define DLM_WAIT_VM(n) \
+  __builtin_amdgcn_s_waitcnt((((n)&15) | (((n) >> 4) << 14)) | (0x7 << 4) | (0xF << 8))
+
+// Lane -> (row, chunk) map of DMA instruction i of wave w: 8 rows of 128 B;
+// lane l covers row (w*I + i)*8 + l/8, physical chunk l%8, which holds the
+// logical K chunk (l%8) ^ ((row >> 1) & 7).
+__device__ __forceinline__ int dma_row(int wave, int I, int i, int lane) {
+  return (wave * I + i) * 8 + (lane >> 3);
+}
+__device__ __forceinline__ int dma_chunk(int row, int lane) { return (lane & 7) ^ ((row >> 1) & 7); }
+
+template <int I>
+struct RowDma {
+  i32x4 rs;
+  int base[I];  // byte offset of the lane's chunk in K-slice 0, -1 past the last row
+  int kc[I];    // K index of that chunk within a slice
+  int K;
+  __device__ RowDma(const RowDesc& d, int r0, int wave, int lane)
+      : rs(dma_rsrc(d.p, d.bytes)), K(d.K) {
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const int row = dma_row(wave, I, i, lane);
+      const int c = dma_chunk(row, lane);
+      kc[i] = c * 8;
+      base[i] = r0 + row < d.rows ? ((r0 + row) * d.ld + c * 8) * 2 : -1;
+    }
+  }
+  __device__ __forceinline__ void prepare(int) {}
+  __device__ __forceinline__ int off(int i, int kt) const {
+    return (base[i] >= 0 && kt * BK + kc[i] < K) ? base[i] + kt * (BK * 2) : kOOB;
+  }
+};
+
+// Implicit-im2col rows for the DMA path (C0, C0a, C1, C1a multiples of 64:
+// one tap and one source per K slice, both wave-uniform).  Every parameter is
+// copied into registers (the DMA asm clobbers memory, which would otherwise
+// force kernel-argument reloads inside the loop) and the per-lane offset is
+// computed with selects only.
+__device__ __forceinline__ int rfl(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <int I>
+struct ConvDma {
+  int pbase[I], ihb[I], iwb[I], mrow[I], cch[I];
+  // uniform parameters
+  const f16 *s0a, *s0b, *s1a, *s1b;
+  unsigned bytes0a, bytes0b, bytes1a, bytes1b;
+  int C0, C0a, ld0a, ld0b, C1, C1a, ld1a, ld1b, K0, KW, Hv, Wv, W, up, M;
+  // per-slice state
+  i32x4 rs;
+  int seg, kh, kw, ld, cbase;
+  __device__ ConvDma(const ConvParams& d, int m0, int wave, int lane)
+      : s0a(d.s0a), s0b(d.s0b), s1a(d.s1a), s1b(d.s1b), bytes0a(d.bytes0a), bytes0b(d.bytes0b),
+        bytes1a(d.bytes1a), bytes1b(d.bytes1b), C0(d.C0), C0a(d.C0a), ld0a(d.ld0a), ld0b(d.ld0b),
+        C1(d.C1), C1a(d.C1a), ld1a(d.ld1a), ld1b(d.ld1b), K0(d.K0), KW(d.KW), Hv(d.Hv), Wv(d.Wv),
+        W(d.W), up(d.up), M(d.M) {
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const int row = dma_row(wave, I, i, lane);
+      cch[i] = dma_chunk(row, lane) * 8;
+      const int m = m0 + row;
+      mrow[i] = m;
+      const int mm = m < d.M ? m : 0;
+      const int n = mm / d.HoWo;
+      const int q = mm - n * d.HoWo;
+      const int oh = q / d.Wo;
+      const int ow = q - oh * d.Wo;
+      pbase[i] = m < d.M ? n * d.H * d.W : -1;
+      ihb[i] = oh * d.stride - d.pad;
+      iwb[i] = ow * d.stride - d.pad;
+    }
+  }
+  __device__ __forceinline__ void prepare(int kt) {
+    const int k0 = kt * BK;
+    seg = k0 < K0 ? 0 : 1;
+    const int tap = k0 / C0;  // only meaningful in segment 0
+    const int c = k0 - tap * C0;
+    const int cs = k0 - K0;   // only meaningful in segment 1
+    const bool isa0 = c < C0a, isa1 = cs < C1a;
+    const bool s1 = seg != 0;
+    const f16* src = s1 ? pick(isa1, s1a, s1b) : pick(isa0, s0a, s0b);
+    const unsigned bytes = s1 ? pick(isa1, bytes1a, bytes1b) : pick(isa0, bytes0a, bytes0b);
+    rs = dma_rsrc(src, bytes);
+    ld = rfl(s1 ? pick(isa1, ld1a, ld1b) : pick(isa0, ld0a, ld0b));
+    cbase = rfl(s1 ? pick(isa1, cs, cs - C1a) : pick(isa0, c, c - C0a));
+    const int khh = tap / KW;
+    kh = rfl(s1 ? cs : khh);  // segment 1: K index of the slice, for the tail check
+    kw = rfl(s1 ? 0 : tap - khh * KW);
+    seg = rfl(seg);
+  }
+  __device__ __forceinline__ int off(int i, int) const {
+    int ih = ihb[i] + kh, iw = iwb[i] + kw;
+    const bool ok0 = (pbase[i] >= 0) & ((unsigned)ih < (unsigned)Hv) & ((unsigned)iw < (unsigned)Wv);
+    ih >>= up;
+    iw >>= up;
+    const int o0 = ((pbase[i] + ih * W + iw) * ld + cbase + cch[i]) * 2;
+    const bool ok1 = (mrow[i] < M) & (kh + cch[i] < C1);
+    const int o1 = (mrow[i] * ld + cbase + cch[i]) * 2;
+    return seg ? (ok1 ? o1 : kOOB) : (ok0 ? o0 : kOOB);
+  }
+};
+
+template <class Desc>
+struct DmaOf;
+template <>
+struct DmaOf<RowDesc> {
+  template <int I>
+  using T = RowDma<I>;
+};
+template <>
+struct DmaOf<ConvDesc> {
+  template <int I>
+  using T = ConvDma<I>;
+};
+
+__device__ __forceinline__ f16x4 ld4h(const f16* p) { return *reinterpret_cast<const f16x4*>(p); }
+
+// Epilogue of four consecutive output columns [col, col+4) of one row.
+__device__ __forceinline__ void epi4(const f32x16& a, int q, int row, int col, const EpiArgs& ep) {
+  if (row >= ep.M || col >= ep.N) return;
+  float v[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) v[t] = a[4 * q + t] * ep.alpha;
+  if (ep.bias) {
+    const f16x4 b = ld4h(ep.bias + col);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] += (float)b[t];
+  }
+  int n = 0, p = row;
+  if (ep.rows_per_sample > 0) {
+    n = row / ep.rows_per_sample;
+    p = row - n * ep.rows_per_sample;
+  }
+  if (ep.tbias) {
+    const f16x4 b = ld4h(ep.tbias + (size_t)n * ep.tbias_ld + col);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] += (float)b[t];
+  }
+  if (ep.act == DLM_ACT_SILU) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = silu_f(v[t]);
+  } else if (ep.act == DLM_ACT_GELU) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = gelu_erf_f(v[t]);
+  }
+  if (ep.res) {
+    const f16x4 r = ld4h(ep.res + (size_t)row * ep.ldr + col);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)r[t];
+  }
+  if (ep.out_nchw) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ep.y[((size_t)n * ep.N + col + t) * ep.rows_per_sample + p] = (f16)v[t];
+  } else {
+    const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *reinterpret_cast<f16x4*>(ep.y + (size_t)row * ep.ldy + col) = o;
+  }
+}
+
+// GEGLU epilogue: value block av and gate block ag of the same 32 output
+// columns; col is the packed value column, ocol the output column.
+__device__ __forceinline__ void epi4_geglu(const f32x16& av, const f32x16& ag, int q, int row,
+                                           int col, int ocol, const EpiArgs& ep) {
+  if (row >= ep.M || col >= ep.N) return;
+  float v[4], g[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    v[t] = av[4 * q + t] * ep.alpha;
+    g[t] = ag[4 * q + t] * ep.alpha;
+  }
+  if (ep.bias) {
+    const f16x4 bv = ld4h(ep.bias + col), bg = ld4h(ep.bias + col + 32);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      v[t] += (float)bv[t];
+      g[t] += (float)bg[t];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) v[t] *= gelu_erf_f(g[t]);
+  if (ep.res) {
+    const f16x4 r = ld4h(ep.res + (size_t)row * ep.ldr + ocol);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)r[t];
+  }
+  const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+  *reinterpret_cast<f16x4*>(ep.y + (size_t)row * ep.ldy + ocol) = o;
+}
+
+template <int BM, int BN, int WM, int WN, int NS, class Desc>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
+  constexpr int WAVES_N = BN / WN;
+  constexpr int NW = (BM / WM) * WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int SA = BM * BK * 2;
+  constexpr int STAGE = (BM + BN) * BK * 2;
+  constexpr int IA = BM * 8 / 64 / NW, IB = BN * 8 / 64 / NW;  // DMA instructions per wave per slice
+  static_assert(IA * NW * 64 == BM * 8 && IB * NW * 64 == BN * 8, "tile/DMA split");
+  static_assert(NS >= 2, "at least two slices");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem_generic[NS * STAGE];
+  unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_generic;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  int tmi, tni;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+
+  typename DmaOf<Desc>::template T<IA> al(ad, m0, wave, lane);
+  RowDma<IB> bl(bd, n0, wave, lane);
+  const int nk = (bd.K + BK - 1) / BK;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  auto frag = [&](const unsigned char DLM_LDS* st, int row, int ks) -> f16x8 {
+    const int c = (2 * ks + (lane >> 5)) ^ ((row >> 1) & 7);
+    return *reinterpret_cast<const f16x8 DLM_LDS*>(st + row * 128 + c * 16);
+  };
+  auto issue_all = [&](int buf, int kt) {
+    unsigned char DLM_LDS* st = smem + buf * STAGE;
+    al.prepare(kt);
+#pragma unroll
+    for (int i = 0; i < IA; ++i) dma16(al.rs, st + (wave * IA + i) * 1024, al.off(i, kt));
+#pragma unroll
+    for (int i = 0; i < IB; ++i) dma16(bl.rs, st + SA + (wave * IB + i) * 1024, bl.off(i, kt));
+  };
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue_all(s, min(s, nk - 1));
+
+  constexpr int VM = (NS - 2) * (IA + IB);
+  for (int kt = 0; kt < nk; ++kt) {
+    DLM_WAIT_VM(VM);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char DLM_LDS* st = smem + (kt % NS) * STAGE;
+    unsigned char DLM_LDS* nst = smem + ((kt + NS - 1) % NS) * STAGE;
+    const int nkt = min(kt + NS - 1, nk - 1);
+    al.prepare(nkt);
+    f16x8 fa[2][TM], fb[2][TN];
+    auto rd = [&](int ks) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[ks & 1][i] = frag(st, wm * WM + i * 32 + (lane & 31), ks);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[ks & 1][j] = frag(st + SA, wn * WN + j * 32 + (lane & 31), ks);
+    };
+    rd(0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < BK / 16) rd(ks + 1);
+#pragma unroll
+      for (int i = 0; i < IA; ++i)
+        if (i % (BK / 16) == ks) dma16(al.rs, nst + (wave * IA + i) * 1024, al.off(i, nkt));
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+        if (i % (BK / 16) == ks) dma16(bl.rs, nst + SA + (wave * IB + i) * 1024, bl.off(i, nkt));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  DLM_WAIT_VM(0);  // no DMA may still be writing this workgroup's LDS at exit
+
+  // ------------------------------ epilogue ------------------------------
+  const int row0 = m0 + wm * WM + (lane & 31);
+  const int col0 = n0 + wn * WN + 4 * (lane >> 5);
+  if constexpr (TN % 2 == 0) {
+    if (ep.act == DLM_ACT_GEGLU) {
+      const int ocol0 = (n0 + wn * WN) / 2 + 4 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; j += 2)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            epi4_geglu(acc[i][j], acc[i][j + 1], q, row0 + i * 32, col0 + j * 32 + 8 * q,
+                       ocol0 + (j / 2) * 32 + 8 * q, ep);
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) epi4(acc[i][j], q, row0 + i * 32, col0 + j * 32 + 8 * q, ep);
+}
+
 // ---------------------------------------------------------------------------
 // Host-side tile configuration choice and launch.
 // ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, int NS, class Desc>
+static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
+                      hipStream_t s) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, Desc>), dim3(tiles_m * tiles_n),
+                     dim3(NT), 0, s, ad, bd, ep, tiles_m, tiles_n);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
 template <int BM, int BN, int WM, int WN, bool DEEP = true, class Desc>
 static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                       hipStream_t s) {
@@ -478,10 +857,68 @@ static inline long long ceil_div(long long a, long long b) { return (a + b - 1) 
 // Tile-shape override for tuning sweeps (0 = automatic choice).
 static int g_forced_tile = 0;
 
+static bool al8(const void* p) { return ((uintptr_t)p & 7) == 0; }
+
+// The DMA core needs 16-byte aligned operands (true of every RowDesc/ConvDesc
+// the entry points accept), whole 4-column output groups and 8-byte aligned
+// epilogue vectors.
+static bool dma_epilogue_ok(const EpiArgs& ep) {
+  if (ep.N % 4 != 0 || !al8(ep.y) || (ep.bias && !al8(ep.bias))) return false;
+  if (!ep.out_nchw && ep.ldy % 4 != 0) return false;
+  if (ep.res && (ep.ldr % 4 != 0 || !al8(ep.res))) return false;
+  if (ep.tbias && (ep.tbias_ld % 4 != 0 || !al8(ep.tbias))) return false;
+  return true;
+}
+static bool dma_operand_ok(const RowDesc& a) { return dlm_aligned16(a.p) && a.ld % 8 == 0; }
+static bool dma_operand_ok(const ConvDesc& d) {
+  return !d.generic && d.C1 % BK == 0 && d.C1a % BK == 0;
+}
+
 template <class Desc>
 static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                        hipStream_t s) {
   constexpr int kCUs = 256;
+  const bool dma = dma_epilogue_ok(ep) && dma_operand_ok(ad) && dma_operand_ok(bd);
+  if (dma) {
+    // GEGLU pairs value/gate blocks inside one wave: only 64-column waves
+    switch (ep.act == DLM_ACT_GEGLU &&
+                    (g_forced_tile == 9 || g_forced_tile == 11 || g_forced_tile == 14 || g_forced_tile == 15)
+                ? 0
+                : g_forced_tile) {
+      case 8: return launch_dma<128, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
+      case 9: return launch_dma<128, 64, 64, 32, 2>(ad, bd, ep, M, N, s);
+      case 10: return launch_dma<128, 128, 64, 64, 4>(ad, bd, ep, M, N, s);
+      case 11: return launch_dma<128, 64, 64, 32, 4>(ad, bd, ep, M, N, s);
+      case 12: return launch_dma<64, 128, 32, 64, 2>(ad, bd, ep, M, N, s);
+      case 13: return launch_dma<256, 128, 128, 64, 2>(ad, bd, ep, M, N, s);
+      case 14: return launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
+      case 15: return launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s);
+      case 16: return launch_dma<256, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
+      case 17: return launch_dma<128, 128, 32, 64, 4>(ad, bd, ep, M, N, s);
+      default: break;
+    }
+    if (g_forced_tile == 0 || ep.act == DLM_ACT_GEGLU) {
+      // Measured on the UNet's shapes: 8-wave 128x128 tiles (two waves per
+      // SIMD) everywhere; two slices in flight when at least one tile per CU
+      // exists (two workgroups per CU then hide each other's latency), a
+      // four-slice ring when the grid leaves CUs with a single workgroup.
+      // GEGLU needs 64-column waves (value and gate blocks in one wave).
+      const long long t128 = ceil_div(M, 128) * ceil_div(N, 128);
+      if (ep.act == DLM_ACT_GEGLU)
+        return t128 >= kCUs ? launch_dma<128, 128, 64, 64, 2>(ad, bd, ep, M, N, s)
+                            : launch_dma<128, 128, 32, 64, 4>(ad, bd, ep, M, N, s);
+      if (t128 >= kCUs / 2) {
+        if (N % 128 != 0)
+          return ceil_div(M, 128) * ceil_div(N, 64) >= kCUs
+                     ? launch_dma<128, 64, 64, 32, 2>(ad, bd, ep, M, N, s)
+                     : launch_dma<128, 64, 64, 32, 4>(ad, bd, ep, M, N, s);
+        return t128 >= kCUs ? launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s)
+                            : launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
+      }
+      // fewer than 128 tiles of 128x128: the small-tile kernel below
+    }
+  }
+  if (ep.act == DLM_ACT_GEGLU) return launch_cfg<128, 128, 64, 64>(ad, bd, ep, M, N, s);
   switch (g_forced_tile) {
     case 1: return launch_cfg<128, 128, 64, 64>(ad, bd, ep, M, N, s);
     case 2: return launch_cfg<128, 64, 64, 32>(ad, bd, ep, M, N, s);
@@ -588,13 +1025,13 @@ __global__ void conv_weight_pack_kernel(const f16* __restrict__ w, f16* __restri
   }
 }
 
-// GEGLU interleave: packed row 32q+s <- value row 16q+s (s<16) or gate row
-// d+16q+s-16 (s>=16).
+// GEGLU interleave in 32-row block pairs: packed row 64p+s <- value row
+// 32p+s (s<32) or gate row d+32p+s-32 (s>=32).
 __global__ void geglu_pack_kernel(const f16* __restrict__ w, const f16* __restrict__ b,
                                   f16* __restrict__ wo, f16* __restrict__ bo, int d, int K) {
   const int r = blockIdx.x;  // packed row
-  const int q = r >> 5, s = r & 31;
-  const int src = s < 16 ? 16 * q + s : d + 16 * q + (s - 16);
+  const int q = r >> 6, s = r & 63;
+  const int src = s < 32 ? 32 * q + s : d + 32 * q + (s - 32);
   for (int k = threadIdx.x; k < K; k += blockDim.x) wo[(size_t)r * K + k] = w[(size_t)src * K + k];
   if (threadIdx.x == 0 && b && bo) bo[r] = b[src];
 }
@@ -716,7 +1153,7 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
               "X or W larger than 2 GiB");
   DLM_REQUIRE(act >= DLM_ACT_NONE && act <= DLM_ACT_GELU, "unknown act");
   if (act == DLM_ACT_GEGLU) {
-    DLM_REQUIRE(N % 32 == 0, "GEGLU needs N (interleaved value+gate columns) % 32 == 0");
+    DLM_REQUIRE(N % 64 == 0, "GEGLU needs N (interleaved value+gate columns) % 64 == 0");
     DLM_REQUIRE(ldy >= N / 2, "ldy smaller than N/2");
     DLM_REQUIRE(!R || ldr >= N / 2, "ldr smaller than N/2");
   } else {
@@ -777,7 +1214,7 @@ int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias
                         void* stream) {
   if (d <= 0 || K <= 0) return DLM_OK;
   DLM_REQUIRE(w && w_out, "NULL pointer");
-  DLM_REQUIRE(d % 16 == 0, "d must be a multiple of 16");
+  DLM_REQUIRE(d % 32 == 0, "d must be a multiple of 32");
   hipLaunchKernelGGL(geglu_pack_kernel, dim3(2 * d), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)w, (const f16*)bias, (f16*)w_out, (f16*)bias_out, d, K);
   DLM_LAUNCH_CHECK();
@@ -913,7 +1350,7 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
 }  // extern "C"
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 7, "tile_id must be in [0, 7]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 17, "tile_id must be in [0, 17]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

@@ -153,9 +153,9 @@ int dlm_gemm_force_tile(int tile_id);
 /* Epilogue activation codes. */
 #define DLM_ACT_NONE 0
 #define DLM_ACT_SILU 1
-/* GEGLU: the weight rows (and bias) are interleaved in blocks of 16
- * (16 value rows, then the 16 matching gate rows, see dlm_geglu_pack_fp16);
- * the output has N/2 columns: out = value * gelu_erf(gate). */
+/* GEGLU: the weight rows (and bias) are interleaved in blocks of 32
+ * (32 value rows, then the 32 matching gate rows, see dlm_geglu_pack_fp16);
+ * the output has N/2 columns: out = value * gelu_erf(gate).  N % 64 == 0. */
 #define DLM_ACT_GEGLU 2
 #define DLM_ACT_GELU 3
 
@@ -171,7 +171,8 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
                     float alpha, float beta, int act, void* stream);
 
 /* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
- * diffusers stores them) into the 16-row interleave DLM_ACT_GEGLU expects. */
+ * diffusers stores them) into the 32-row interleave DLM_ACT_GEGLU expects
+ * (d % 32 == 0). */
 int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias_out,
                         int d, int K, void* stream);
 
