@@ -53,6 +53,18 @@ class AttentionArgs(ctypes.Structure):
     ]
 
 
+class AttentionVtArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", P), ("k", P), ("vt", P), ("o", P),
+        ("q_sb", LL), ("q_ss", LL), ("q_sh", LL),
+        ("k_sb", LL), ("k_ss", LL), ("k_sh", LL),
+        ("vt_sb", LL), ("vt_sh", LL),
+        ("o_sb", LL), ("o_ss", LL), ("o_sh", LL),
+        ("vt_ld", I), ("B", I), ("H", I), ("Sq", I), ("Sk", I), ("scale", F),
+        ("k_bytes", ctypes.c_ulonglong), ("vt_bytes", ctypes.c_ulonglong),
+    ]
+
+
 # name -> (restype, argtypes); every int-returning entry point is a status.
 HIP_SIGNATURES = {
     "dlm_last_error": (c_char_p, []),
@@ -100,6 +112,8 @@ HIP_SIGNATURES = {
     "dlm_group_norm_nhwc_workspace_bytes": (c_size_t, [I, I, I]),
     "dlm_group_norm_nhwc_fp16": (I, [P, I, I, P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
     "dlm_attention_strided_fp16": (I, [POINTER(AttentionArgs), P]),
+    "dlm_attention_vt_fp16": (I, [POINTER(AttentionVtArgs), P]),
+    "dlm_linear_vt_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, I, P]),
     "dlm_sdxl_embed_inputs_fp16": (I, [P, P, I, P, I, I, P, I, P, I, P]),
     "dlm_linear_small_fp16": (I, [P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),

@@ -199,6 +199,282 @@ __global__ void __launch_bounds__(256) flash_attn_d64_kernel(AttnParams p) {
   }
 }
 
+// ===========================================================================
+// Flash attention over a transposed V (V^T[b][h][d][key]).
+//
+// Same lane-per-query formulation as above (S^T = K Q^T, O^T = V^T P^T), but
+//   * K and V^T tiles of 64 keys are copied global -> LDS by DMA
+//     (buffer_load ... lds) into a three-tile ring, rows of 128 B with the
+//     16-byte chunks XOR-swizzled by (row >> 1) & 7, so every fragment is one
+//     conflict-free ds_read_b128 and no VGPR staging or LDS transpose exists;
+//   * K rows are placed in LDS in a fixed permutation (rows 4..7 and 8..11 of
+//     every 16 swapped), chosen so that the eight exponentiated scores a lane
+//     feeds to one P^T fragment belong to eight consecutive keys: the matching
+//     V^T fragment is then 16 contiguous bytes of a V^T row;
+//   * each wave owns QB blocks of 32 queries, sharing every K and V^T
+//     fragment read between them;
+//   * the running max is kept on raw scores, p = 2^(s*c - m*c) is one FMA and
+//     one v_exp_f32 (c = scale * log2 e); masking runs only on a partial last
+//     key tile.
+// ===========================================================================
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define DLM_LDS __attribute__((address_space(3)))
+
+struct FlashVtParams {
+  const f16* q;
+  const f16* k;
+  const f16* vt;
+  f16* o;
+  long long q_sb, q_ss, q_sh;
+  long long k_sb, k_ss, k_sh;
+  long long vt_sb, vt_sh;  // element offset of head (b, h) in V^T; row d at + d * vt_ld
+  long long o_sb, o_ss, o_sh;
+  int vt_ld;
+  int Sq, Sk;
+  float c;                  // scale * log2(e)
+  unsigned k_bytes, vt_bytes;
+};
+
+__device__ __forceinline__ i32x4 fa_rsrc(const void* p, unsigned bytes) {
+  const uint64_t a = (uint64_t)p;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// M0 carries the LDS destination; nothing else in this file uses M0 (the
+// compiler's own code never reads it here), so the clobber is safe even
+// though the compiler treats M0 as reserved.
+__device__ __forceinline__ void fa_dma16(const i32x4& r, const unsigned char DLM_LDS* dst, int voff) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
+               "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+
+#define FA_WAIT_VM(n) \
+  __builtin_amdgcn_s_waitcnt((((n)&15) | (((n) >> 4) << 14)) | (0x7 << 4) | (0xF << 8))
+
+// LDS row r of a K tile holds key fa_perm(r) of the tile.
+__device__ __forceinline__ int fa_perm(int r) {
+  const int q = r & 12;
+  return (q == 4 || q == 8) ? (r ^ 12) : r;
+}
+
+constexpr int FA_TK = 64;             // keys per tile
+constexpr int FA_TILE = FA_TK * 128;  // bytes of one K (or V^T) tile
+constexpr int FA_STAGE = 2 * FA_TILE;
+constexpr int FA_NS = 3;
+constexpr int kFaOOB = (int)0x80000000;
+
+template <int QB>
+__global__ void __launch_bounds__(256) flash_vt_kernel(FlashVtParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem_g[FA_NS * FA_STAGE];
+  unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_g;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5;
+  const int q0 = blockIdx.x * (128 * QB) + wave * (32 * QB);
+
+  f16x8 qf[QB][4];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = q0 + qb * 32 + (lane & 31);
+    const f16* qp = p.q + b * p.q_sb + h * p.q_sh + (long long)qi * p.q_ss + g * 8;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      qf[qb][ds] = qi < p.Sq ? *reinterpret_cast<const f16x8*>(qp + ds * 16) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  // DMA map: each tile is 64 rows x 8 chunks; wave w copies rows
+  // (w*2 + i)*8 + lane/8, i = 0, 1, of both the K and the V^T tile.
+  const i32x4 rk = fa_rsrc(p.k, p.k_bytes);
+  const i32x4 rv = fa_rsrc(p.vt, p.vt_bytes);
+  int koff[2], kkey[2], voff[2], vkey[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (wave * 2 + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    kkey[i] = fa_perm(r);
+    koff[i] = (int)((b * p.k_sb + h * p.k_sh + (long long)kkey[i] * p.k_ss + c * 8) * 2);
+    vkey[i] = c * 8;
+    voff[i] = (int)((b * p.vt_sb + h * p.vt_sh + (long long)r * p.vt_ld + c * 8) * 2);
+  }
+  const int kstep = (int)(FA_TK * p.k_ss * 2);
+  auto issue = [&](int buf, int kt) {
+    unsigned char DLM_LDS* st = smem + buf * FA_STAGE;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = kt * FA_TK + kkey[i];
+      fa_dma16(rk, st + (wave * 2 + i) * 1024, key < p.Sk ? koff[i] + kt * kstep : kFaOOB);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = kt * FA_TK + vkey[i];
+      fa_dma16(rv, st + FA_TILE + (wave * 2 + i) * 1024, key < p.Sk ? voff[i] + kt * (FA_TK * 2) : kFaOOB);
+    }
+  };
+  auto frag = [&](const unsigned char DLM_LDS* st, int row, int chunk) -> f16x8 {
+    const int c = chunk ^ ((row >> 1) & 7);
+    return *reinterpret_cast<const f16x8 DLM_LDS*>(st + row * 128 + c * 16);
+  };
+
+  const int nkt = (p.Sk + FA_TK - 1) / FA_TK;
+  issue(0, 0);
+  issue(1, min(1, nkt - 1));
+
+  float m_run[QB], l_run[QB];
+  f32x16 o[2][QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      o[0][qb][e] = 0.0f;
+      o[1][qb][e] = 0.0f;
+    }
+  }
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    FA_WAIT_VM(4);  // the tile issued two iterations ago (four DMA per wave per tile)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char DLM_LDS* st = smem + (kt % FA_NS) * FA_STAGE;
+    issue((kt + 2) % FA_NS, min(kt + 2, nkt - 1));
+
+    // S^T = K Q^T: s[kb][qb], lane = query, element e = LDS key row
+    // kb*32 + 8*(e>>2) + 4g + (e&3)
+    f32x16 s[2][QB];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][qb][e] = 0.0f;
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) {
+        const f16x8 kf = frag(st, kb * 32 + (lane & 31), 2 * ds + g);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) s[kb][qb] = mfma32x32x16(kf, qf[qb][ds], s[kb][qb]);
+      }
+    }
+    if (kt * FA_TK + FA_TK > p.Sk) {  // partial last tile: keys past Sk do not exist
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kt * FA_TK + fa_perm(kb * 32 + mfma_row(e, lane));
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            if (key >= p.Sk) s[kb][qb][e] = -INFINITY;
+        }
+    }
+
+    // Lazy rescale: the reference max m_run only moves when some lane's tile
+    // max exceeds it by more than 2^8 in the exp2 domain (a wave-uniform and,
+    // after the first tiles, rare branch); otherwise p = 2^((s - m_run) c)
+    // stays <= 256, exact in fp16 and harmless in the fp32 sums.
+    f16x8 pf[4][QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mt = s[0][qb][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][qb][e]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const bool grow = (mt - m_run[qb]) * p.c > 8.0f;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = fmaxf(m_run[qb], mt);
+        const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_new) * p.c);
+        m_run[qb] = m_new;
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          o[0][qb][e] *= alpha;
+          o[1][qb][e] *= alpha;
+        }
+      }
+      const float mc = m_run[qb] * p.c;
+      float lsum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][e], p.c, -mc));
+          lsum += pe;
+          pf[kb * 2 + (e >> 3)][qb][e & 7] = (f16)pe;
+        }
+      l_run[qb] += lsum;
+    }
+
+    // O^T += V^T P^T over four 16-key steps; step j covers tile keys
+    // 16j + 8g + [0, 8) for lane group g
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const f16x8 vf = frag(st + FA_TILE, dt * 32 + (lane & 31), 2 * j + g);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) o[dt][qb] = mfma32x32x16(vf, pf[j][qb], o[dt][qb]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  FA_WAIT_VM(0);
+
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = q0 + qb * 32 + (lane & 31);
+    const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+    const float inv = 1.0f / l_tot;
+    if (qi < p.Sq) {
+      f16* obase = p.o + b * p.o_sb + h * p.o_sh + (long long)qi * p.o_ss;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          f16x4 r;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) r[t] = (f16)(o[dt][qb][4 * gq + t] * inv);
+          *reinterpret_cast<f16x4*>(obase + dt * 32 + 8 * gq + 4 * g) = r;
+        }
+    }
+  }
+}
+
+int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
+  FlashVtParams p;
+  p.q = (const f16*)a->q;
+  p.k = (const f16*)a->k;
+  p.vt = (const f16*)a->vt;
+  p.o = (f16*)a->o;
+  p.q_sb = a->q_sb; p.q_ss = a->q_ss; p.q_sh = a->q_sh;
+  p.k_sb = a->k_sb; p.k_ss = a->k_ss; p.k_sh = a->k_sh;
+  p.vt_sb = a->vt_sb; p.vt_sh = a->vt_sh; p.vt_ld = a->vt_ld;
+  p.o_sb = a->o_sb; p.o_ss = a->o_ss; p.o_sh = a->o_sh;
+  p.Sq = a->Sq;
+  p.Sk = a->Sk;
+  p.c = a->scale * 1.4426950408889634f;
+  p.k_bytes = (unsigned)a->k_bytes;
+  p.vt_bytes = (unsigned)a->vt_bytes;
+  const long long wg2 = (long long)((a->Sq + 255) / 256) * a->H * a->B;
+  if (wg2 >= 256) {
+    const dim3 grid((a->Sq + 255) / 256, a->H, a->B);
+    hipLaunchKernelGGL(flash_vt_kernel<2>, grid, dim3(256), 0, s, p);
+  } else {
+    const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
+    hipLaunchKernelGGL(flash_vt_kernel<1>, grid, dim3(256), 0, s, p);
+  }
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
 int attention_strided(const dlm_attention_args* a, hipStream_t s) {
   AttnParams p;
   p.q = (const f16*)a->q;
@@ -240,6 +516,31 @@ int dlm_attention_strided_fp16(const dlm_attention_args* a, void* stream) {
                   a->o_sb % 4 == 0 && a->o_ss % 4 == 0 && a->o_sh % 4 == 0,
               "strides must keep 16-byte (Q/K/V) and 8-byte (O) alignment");
   return attention_strided(a, (hipStream_t)stream);
+}
+
+int dlm_attention_vt_fp16(const dlm_attention_vt_args* a, void* stream) {
+  DLM_REQUIRE(a != nullptr, "args is NULL");
+  if (a->B <= 0 || a->H <= 0 || a->Sq <= 0 || a->Sk <= 0) return DLM_OK;
+  DLM_REQUIRE(a->q && a->k && a->vt && a->o, "NULL operand");
+  DLM_REQUIRE(dlm_aligned16(a->q) && dlm_aligned16(a->k) && dlm_aligned16(a->vt) &&
+                  ((uintptr_t)a->o & 7) == 0,
+              "Q/K/V^T must be 16-byte aligned, O 8-byte aligned");
+  DLM_REQUIRE(stride_ok(a->q_sb) && stride_ok(a->q_ss) && stride_ok(a->q_sh) &&
+                  stride_ok(a->k_sb) && stride_ok(a->k_ss) && stride_ok(a->k_sh) &&
+                  stride_ok(a->vt_sb) && stride_ok(a->vt_sh) && a->vt_ld % 8 == 0 &&
+                  a->o_sb % 4 == 0 && a->o_ss % 4 == 0 && a->o_sh % 4 == 0,
+              "strides must keep 16-byte (Q/K/V^T) and 8-byte (O) alignment");
+  DLM_REQUIRE(a->Sk % 8 == 0 && a->vt_ld >= a->Sk, "Sk must be a multiple of 8 and vt_ld >= Sk");
+  DLM_REQUIRE(a->k_bytes > 0 && a->k_bytes < (1ull << 31) && a->vt_bytes > 0 &&
+                  a->vt_bytes < (1ull << 31),
+              "K and V^T buffers must be non-empty and smaller than 2 GiB");
+  // every DMA offset must stay below 2^31: the last head's last key row
+  const long long klast =
+      ((a->B - 1) * a->k_sb + (a->H - 1) * a->k_sh + (long long)(a->Sk - 1) * a->k_ss + 64) * 2;
+  const long long vlast = ((a->B - 1) * a->vt_sb + (a->H - 1) * a->vt_sh + 63LL * a->vt_ld + a->Sk) * 2;
+  DLM_REQUIRE(klast <= (long long)a->k_bytes && vlast <= (long long)a->vt_bytes,
+              "K or V^T extends past its buffer size");
+  return attention_vt(a, (hipStream_t)stream);
 }
 
 int dlm_attention_fp16(const void* q, const void* k, const void* v, void* out, int B, int H,

@@ -44,6 +44,11 @@ struct EpiArgs {
   int out_nchw;
   int M;
   int N;
+  // transposed-V output (DMA core only): columns >= vt_col0 of row m go to
+  // vt[((m / vt_tokens) * (N - vt_col0) + col - vt_col0) * vt_tokens + m % vt_tokens]
+  f16* vt;
+  int vt_col0;
+  int vt_tokens;
 };
 
 // ---------------------------------------------------------------------------
@@ -516,6 +521,8 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void* p, unsigned bytes) {
 // of the buffer and the hardware writes them to LDS at dst + 16 l (dst goes
 // through M0).  Issued as inline asm so the compiler neither tracks nor
 // drains it: the kernel orders it with explicit vmcnt waits and barriers.
+// Nothing else in this file uses M0, so clobbering it is safe although the
+// compiler warns that it treats M0 as reserved.
 __device__ __forceinline__ void dma16(const i32x4& r, const unsigned char DLM_LDS* dst, int voff) {
   const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)dst);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds),
@@ -674,7 +681,13 @@ __device__ __forceinline__ void epi4(const f32x16& a, int q, int row, int col, c
 #pragma unroll
     for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)r[t];
   }
-  if (ep.out_nchw) {
+  if (ep.vt && col >= ep.vt_col0) {
+    const int smp = row / ep.vt_tokens;
+    f16* dst = ep.vt + ((size_t)smp * (ep.N - ep.vt_col0) + (col - ep.vt_col0)) * ep.vt_tokens +
+               (row - smp * ep.vt_tokens);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dst[(size_t)t * ep.vt_tokens] = (f16)v[t];
+  } else if (ep.out_nchw) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) ep.y[((size_t)n * ep.N + col + t) * ep.rows_per_sample + p] = (f16)v[t];
   } else {
@@ -915,9 +928,12 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
         return t128 >= kCUs ? launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s)
                             : launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
       }
+      if (ep.vt)  // the transposed-V epilogue exists only in the DMA core
+        return launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
       // fewer than 128 tiles of 128x128: the small-tile kernel below
     }
   }
+  if (ep.vt) return fail(DLM_ERR_UNSUPPORTED, "transposed-V output needs aligned operands");
   if (ep.act == DLM_ACT_GEGLU) return launch_cfg<128, 128, 64, 64>(ad, bd, ep, M, N, s);
   switch (g_forced_tile) {
     case 1: return launch_cfg<128, 128, 64, 64>(ad, bd, ep, M, N, s);
@@ -955,6 +971,9 @@ static EpiArgs make_epi(void* Y, int ldy, const void* bias, const void* R, int l
   ep.out_nchw = 0;
   ep.M = M;
   ep.N = N;
+  ep.vt = nullptr;
+  ep.vt_col0 = 0;
+  ep.vt_tokens = 0;
   return ep;
 }
 
@@ -1162,6 +1181,31 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
   }
   return linear_impl(X, lda, W, ldw, bias, R, ldr, Y, ldy, M, N, K, alpha, beta, act,
                      (hipStream_t)stream);
+}
+
+int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const void* bias, void* Y,
+                       int ldy, void* VT, int vt_col0, int tokens, int M, int N, int K,
+                       void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(X && W && Y && VT, "NULL operand");
+  DLM_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K, lda and ldw must be multiples of 8");
+  DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
+  DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
+  DLM_REQUIRE(2LL * M * lda < (1LL << 31) && 2LL * N * ldw < (1LL << 31),
+              "X or W larger than 2 GiB");
+  DLM_REQUIRE(vt_col0 >= 0 && vt_col0 < N && vt_col0 % 4 == 0 && N % 4 == 0,
+              "vt_col0 must be a multiple of 4 inside [0, N), N % 4 == 0");
+  DLM_REQUIRE(tokens > 0 && M % tokens == 0, "M must be a whole number of samples of `tokens` rows");
+  DLM_REQUIRE(ldy >= vt_col0 && ldy % 4 == 0, "ldy must cover the columns before vt_col0");
+  DLM_REQUIRE(((uintptr_t)Y & 7) == 0 && (!bias || ((uintptr_t)bias & 7) == 0),
+              "Y and bias must be 8-byte aligned");
+  RowDesc ad{(const f16*)X, lda, M, K, (unsigned)((size_t)M * lda * 2)};
+  RowDesc bd{(const f16*)W, ldw, N, K, (unsigned)((size_t)N * ldw * 2)};
+  EpiArgs ep = make_epi(Y, ldy, bias, nullptr, 0, M, N, 1.0f, 0.0f, DLM_ACT_NONE);
+  ep.vt = (f16*)VT;
+  ep.vt_col0 = vt_col0;
+  ep.vt_tokens = tokens;
+  return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
 }
 
 int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, float alpha,

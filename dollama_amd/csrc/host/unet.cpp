@@ -570,7 +570,8 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len
   void* g = sc.alloc<uint16_t>((size_t)M * C);
   void* h = sc.alloc<uint16_t>((size_t)M * C);
   void* n = sc.alloc<uint16_t>((size_t)M * C);
-  void* qkv = sc.alloc<uint16_t>((size_t)M * 3 * C);
+  void* qkv = sc.alloc<uint16_t>((size_t)M * 2 * C);
+  void* vt = sc.alloc<uint16_t>((size_t)M * C);
   void* o = sc.alloc<uint16_t>((size_t)M * C);
   void* f = sc.alloc<uint16_t>((size_t)M * 4 * C);
   const float scale = 1.0f / std::sqrt(64.0f);
@@ -582,18 +583,22 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len
   for (const Block& k : t.blocks) {
     // self-attention
     LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
+    // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
     LAUNCH(kLinear, 2.0 * M * 3 * C * C, 0.0,
-         dlm_linear_fp16(n, C, k.wqkv, C, nullptr, nullptr, 0, qkv, 3 * C, M, 3 * C, C, 1.0f,
-                             0.0f, DLM_ACT_NONE, stream));
+           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, M, 3 * C, C,
+                              stream));
     {
-      dlm_attention_args a{};
+      dlm_attention_vt_args a{};
       const char* base = static_cast<const char*>(qkv);
       a.q = base;
       a.k = base + (size_t)C * kH;
-      a.v = base + (size_t)2 * C * kH;
-      a.q_sb = a.k_sb = a.v_sb = (long long)HW * 3 * C;
-      a.q_ss = a.k_ss = a.v_ss = 3 * C;
-      a.q_sh = a.k_sh = a.v_sh = 64;
+      a.vt = vt;
+      a.q_sb = a.k_sb = (long long)HW * 2 * C;
+      a.q_ss = a.k_ss = 2 * C;
+      a.q_sh = a.k_sh = 64;
+      a.vt_sb = (long long)C * HW;
+      a.vt_sh = 64LL * HW;
+      a.vt_ld = HW;
       a.o = o;
       a.o_sb = (long long)HW * C;
       a.o_ss = C;
@@ -602,10 +607,11 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len
       a.H = heads;
       a.Sq = HW;
       a.Sk = HW;
-      a.Dh = 64;
       a.scale = scale;
+      a.k_bytes = ((size_t)M * 2 * C - C) * kH;
+      a.vt_bytes = (size_t)M * C * kH;
       LAUNCH(kAttention, 4.0 * B * heads * (double)HW * HW * 64, 0.0,
-             dlm_attention_strided_fp16(&a, stream));
+             dlm_attention_vt_fp16(&a, stream));
     }
     LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
          dlm_linear_fp16(o, C, k.wo1, C, k.bo1, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,

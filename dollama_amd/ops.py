@@ -24,7 +24,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import ACT_GEGLU, ACT_GELU, ACT_NONE, ACT_SILU, AttentionArgs, ConvNhwcArgs, call
+from ._lib import (ACT_GEGLU, ACT_GELU, ACT_NONE, ACT_SILU, AttentionArgs, AttentionVtArgs,
+                   ConvNhwcArgs, call)
 
 __all__ = [
     "launch_conv2d", "launch_gemm_fp16", "launch_group_norm", "launch_group_norm_mb",
@@ -273,6 +274,23 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias=None, residual=None, act=ACT_N
     return out
 
 
+def linear_vt(x: torch.Tensor, w: torch.Tensor, vt_col0: int, tokens: int, bias=None):
+    """y = x @ w.T for columns [0, vt_col0) as [M, vt_col0], and the remaining
+    columns transposed per sample as vt [M // tokens, N - vt_col0, tokens]."""
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or M % tokens != 0:
+        raise ValueError("shape mismatch")
+    y = torch.empty(M, vt_col0, dtype=torch.float16, device=x.device)
+    vt = torch.empty(M // tokens, N - vt_col0, tokens, dtype=torch.float16, device=x.device)
+    _need(x, M * K, "x")
+    _need(w, N * K, "w")
+    _need(bias, N, "bias", optional=True)
+    call("dlm_linear_vt_fp16", _p(x), K, _p(w), K, _p(bias), _p(y), vt_col0, _p(vt), vt_col0,
+         tokens, M, N, K, stream_handle())
+    return y, vt
+
+
 def pack_geglu(w: torch.Tensor, b: Optional[torch.Tensor]):
     """[2d, K] value-first GEGLU projection -> 16-row interleave for ACT_GEGLU."""
     two_d, K = w.shape
@@ -408,6 +426,34 @@ def attention_strided(q, k, v, o, *, B, H, Sq, Sk, q_strides, k_strides, v_strid
     a.o, (a.o_sb, a.o_ss, a.o_sh) = _p(o), o_strides
     a.B, a.H, a.Sq, a.Sk, a.Dh, a.scale = B, H, Sq, Sk, Dh, float(scale)
     call("dlm_attention_strided_fp16", ctypes.byref(a), stream_handle())
+    return o
+
+
+def attention_vt(q, k, vt, o, *, B, H, Sq, Sk, q_strides, k_strides, vt_strides, vt_ld,
+                 o_strides, scale):
+    """Flash attention (Dh = 64) with V given transposed: V^T element
+    (b, h, d, key) at vt[b*vt_sb + h*vt_sh + d*vt_ld + key]."""
+    for t, nm in ((q, "q"), (k, "k"), (vt, "vt"), (o, "o")):
+        if not t.is_cuda or t.dtype != torch.float16:
+            raise ValueError(f"{nm} must be a GPU fp16 tensor")
+    def _span(strides, S):
+        sb, ss, sh = strides
+        return (B - 1) * sb + (S - 1) * ss + (H - 1) * sh + 64
+    vspan = (B - 1) * vt_strides[0] + (H - 1) * vt_strides[1] + 63 * vt_ld + Sk
+    for t, span, nm in ((q, _span(q_strides, Sq), "q"), (k, _span(k_strides, Sk), "k"),
+                        (vt, vspan, "vt"), (o, _span(o_strides, Sq), "o")):
+        if t.storage_offset() + span > t.untyped_storage().nbytes() // 2:
+            raise ValueError(f"{nm}: strides reach beyond the tensor's storage")
+    a = AttentionVtArgs()
+    a.q, a.k, a.vt, a.o = _p(q), _p(k), _p(vt), _p(o)
+    a.q_sb, a.q_ss, a.q_sh = q_strides
+    a.k_sb, a.k_ss, a.k_sh = k_strides
+    a.vt_sb, a.vt_sh = vt_strides
+    a.o_sb, a.o_ss, a.o_sh = o_strides
+    a.vt_ld, a.B, a.H, a.Sq, a.Sk, a.scale = vt_ld, B, H, Sq, Sk, float(scale)
+    a.k_bytes = k.untyped_storage().nbytes() - k.storage_offset() * 2
+    a.vt_bytes = vt.untyped_storage().nbytes() - vt.storage_offset() * 2
+    call("dlm_attention_vt_fp16", ctypes.byref(a), stream_handle())
     return o
 
 

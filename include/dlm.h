@@ -170,6 +170,18 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
                     const void* R, int ldr, void* Y, int ldy, int M, int N, int K,
                     float alpha, float beta, int act, void* stream);
 
+/* Linear with a transposed tail: Y = X W^T for columns [0, vt_col0) (row
+ * stride ldy) and, for columns n >= vt_col0, the transpose per sample:
+ * VT[(m / tokens) * (N - vt_col0) + n - vt_col0][m % tokens] (row stride
+ * `tokens`).  Fed with the fused QKV weight [3C, C] and vt_col0 = 2C it
+ * writes Q|K as [M, 2C] and V^T as [B, C, tokens] = [B, H, 64, tokens], the
+ * layout dlm_attention_vt_fp16 reads.  No counterpart in the reference,
+ * which splits heads with separate kernels (k_split_heads,
+ * src/infer/unet.cu:153-278). */
+int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const void* bias, void* Y,
+                       int ldy, void* VT, int vt_col0, int tokens, int M, int N, int K,
+                       void* stream);
+
 /* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
  * diffusers stores them) into the 32-row interleave DLM_ACT_GEGLU expects
  * (d % 32 == 0). */
@@ -234,6 +246,30 @@ typedef struct dlm_attention_args {
   int B; int H; int Sq; int Sk; int Dh; float scale;
 } dlm_attention_args;
 int dlm_attention_strided_fp16(const dlm_attention_args* args, void* stream);
+
+/* Flash attention with V supplied transposed: element (b, h, d, key) of V^T
+ * is at vt[b*vt_sb + h*vt_sh + d*vt_ld + key] (vt_ld >= Sk, multiple of 8).
+ * Q, K, O as in dlm_attention_args; Dh = 64; Sk % 8 == 0.  k_bytes and
+ * vt_bytes bound the K and V^T allocations (each < 2 GiB): reads past them
+ * return zero.  The UNet's QKV projection writes V^T directly (see
+ * dlm_linear_vt_fp16), so self-attention needs no LDS transpose.
+ * Same arithmetic as dlm_attention_fp16 (launch_attention,
+ * src/kernels/attention.cuh:53-73). */
+typedef struct dlm_attention_vt_args {
+  const void* q;
+  const void* k;
+  const void* vt;
+  void* o;
+  long long q_sb, q_ss, q_sh;
+  long long k_sb, k_ss, k_sh;
+  long long vt_sb, vt_sh;
+  long long o_sb, o_ss, o_sh;
+  int vt_ld;
+  int B, H, Sq, Sk;
+  float scale;
+  unsigned long long k_bytes, vt_bytes;
+} dlm_attention_vt_args;
+int dlm_attention_vt_fp16(const dlm_attention_vt_args* args, void* stream);
 
 /* SDXL conditioning inputs on the device (no host round trip, unlike the
  * reference's D2H of time_ids, src/infer/unet.cu:999-1000):

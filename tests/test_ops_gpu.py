@@ -229,6 +229,38 @@ def test_attention_strided_fused_qkv(gpu):
     assert_close(o, ref, "attention strided")
 
 
+@pytest.mark.parametrize("B,H,Sq,Sk", [(1, 1, 32, 64), (1, 2, 300, 136), (2, 10, 4096, 4096),
+                                       (2, 20, 1024, 1024), (1, 3, 1000, 8)])
+def test_attention_vt(gpu, B, H, Sq, Sk):
+    """Flash attention over V^T [B, H, 64, Sk] with Q/K read from a fused
+    [B, S, 2C] buffer; partial last key tiles, Sq not a multiple of the
+    query block, and both query-block widths are covered."""
+    Dh = 64
+    C = H * Dh
+    announce(f"attention_vt B={B} H={H} Sq={Sq} Sk={Sk}")
+    q, k, v = randn((B, H, Sq, Dh), 120), randn((B, H, Sk, Dh), 121), randn((B, H, Sk, Dh), 122)
+    dq = to_gpu(q.permute(0, 2, 1, 3).reshape(B, Sq, C))
+    dk = to_gpu(k.permute(0, 2, 1, 3).reshape(B, Sk, C))
+    vt = to_gpu(v.transpose(2, 3).contiguous())  # [B, H, 64, Sk]
+    o = torch.empty(B, Sq, C, dtype=torch.float16, device=gpu)
+    ops.attention_vt(dq, dk, vt, o, B=B, H=H, Sq=Sq, Sk=Sk, q_strides=(Sq * C, C, Dh),
+                     k_strides=(Sk * C, C, Dh), vt_strides=(H * Dh * Sk, Dh * Sk), vt_ld=Sk,
+                     o_strides=(Sq * C, C, Dh), scale=0.125)
+    ref = torch.cat([R.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], 0.125) for b in range(B)])
+    assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), "attention_vt")
+
+
+@pytest.mark.parametrize("B,S,C", [(2, 1024, 1280), (2, 64, 128), (3, 40, 192)])
+def test_linear_vt(gpu, B, S, C):
+    """Fused QKV projection writing Q|K row-major and V transposed per sample."""
+    announce(f"linear_vt B={B} S={S} C={C}")
+    x, w, b = randn((B * S, C), 130), randn((3 * C, C), 131, 0.05), randn((3 * C,), 132, 0.1)
+    y, vt = ops.linear_vt(to_gpu(x), to_gpu(w), 2 * C, S, bias=to_gpu(b))
+    ref = R.linear(x, w, b)
+    assert_close(y, ref[:, :2 * C], "linear_vt y")
+    assert_close(vt, ref[:, 2 * C:].reshape(B, S, C).transpose(1, 2), "linear_vt vt")
+
+
 # ------------------------------------------------------------ small ops ---
 def test_elementwise_ops(gpu):
     announce("silu/gelu/add/upsample/bias/geglu")
