@@ -35,7 +35,34 @@ def parse():
     ap.add_argument("--loop-steps", type=int, default=20, help="Euler loop length (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-runs", type=int, default=3)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device copy of 256 MiB (5 times), to scale the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a PMC run")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    """A plain device-to-device copy of known size for counter calibration:
+    each of the 5 dispatches reads and writes exactly 256 MiB."""
+    import torch
+    n = 128 << 20  # fp16 elements = 256 MiB
+    a = torch.ones(n, dtype=torch.float16, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes_per_dispatch": 2 * n}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel class, as measured by
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this bench and scaled by the
+    same counters on a plain copy (profiles/hbm_traffic.json)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
 
 
 def cpu_baseline(seed):
@@ -89,6 +116,9 @@ def cpu_baseline(seed):
 
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the UNet step "
               "is not sharded across GPUs in this build.", file=sys.stderr)
@@ -201,14 +231,14 @@ def main():
         "classes": classes,
         "roofline": {
             "bound": "mfma",
-            "kernel": {"conv": "mfma_gemm_kernel<ConvDesc> (implicit-GEMM conv)",
-                       "linear": "mfma_gemm_kernel<RowDesc> (linears)",
-                       "attention": "flash_attn_d64_kernel"}[dom],
+            "kernel": {"conv": "dma_gemm_kernel<ConvDesc> (implicit-GEMM conv, LDS-DMA)",
+                       "linear": "dma_gemm_kernel<RowDesc> (linears, LDS-DMA)",
+                       "attention": "flash_vt_kernel (self) + flash_attn_d64_kernel (cross)"}[dom],
             "achieved": round(achieved, 1),
             "peak": MFMA_FP16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(achieved * 1e12 / MFMA_FP16_PEAK, 4),
-            "traffic": None,
+            "traffic": measured_traffic().get(dom, {}).get("hbm_bytes_per_launch"),
             "launches_per_step": dom_launches,
             "avg_launch_us": round(dom_ms / max(1, dom_launches) * 1e3, 2),
             "flop_per_step": dom_flops,
