@@ -21,6 +21,7 @@
 // implicit im2col gather (zero padding, channel concatenation of two
 // sources, nearest-2x upsampling, a second 1x1 segment) for convolutions.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -603,24 +604,38 @@ struct ConvDma {
       iwb[i] = ow * d.stride - d.pad;
     }
   }
+  // Slices are requested in order (0, 1, ..., then the last one repeated),
+  // so the tap / channel position advances by one slice at a time: no
+  // integer division and no branch in the loop (all selects).
+  int cur_kt = 0, cur_c = 0, cur_kh = 0, cur_kw = 0;
   __device__ __forceinline__ void prepare(int kt) {
+    const bool adv = kt != cur_kt;  // kt == cur_kt + 1
+    int c1 = cur_c + BK;
+    const bool wrap = c1 == C0;
+    c1 = wrap ? 0 : c1;
+    int kw1 = cur_kw + (wrap ? 1 : 0);
+    const bool wrapw = kw1 == KW;
+    kw1 = wrapw ? 0 : kw1;
+    const int kh1 = cur_kh + (wrapw ? 1 : 0);
+    cur_c = rfl(adv ? c1 : cur_c);
+    cur_kw = rfl(adv ? kw1 : cur_kw);
+    cur_kh = rfl(adv ? kh1 : cur_kh);
+    cur_kt = kt;
     const int k0 = kt * BK;
-    seg = k0 < K0 ? 0 : 1;
-    const int tap = k0 / C0;  // only meaningful in segment 0
-    const int c = k0 - tap * C0;
-    const int cs = k0 - K0;   // only meaningful in segment 1
-    const bool isa0 = c < C0a, isa1 = cs < C1a;
-    const bool s1 = seg != 0;
+    const bool s1 = k0 >= K0;
+    const int cs = k0 - K0;  // segment-1 K index of the slice
+    const bool isa0 = cur_c < C0a, isa1 = cs < C1a;
     const f16* src = s1 ? pick(isa1, s1a, s1b) : pick(isa0, s0a, s0b);
     const unsigned bytes = s1 ? pick(isa1, bytes1a, bytes1b) : pick(isa0, bytes0a, bytes0b);
     rs = dma_rsrc(src, bytes);
     ld = rfl(s1 ? pick(isa1, ld1a, ld1b) : pick(isa0, ld0a, ld0b));
-    cbase = rfl(s1 ? pick(isa1, cs, cs - C1a) : pick(isa0, c, c - C0a));
-    const int khh = tap / KW;
-    kh = rfl(s1 ? cs : khh);  // segment 1: K index of the slice, for the tail check
-    kw = rfl(s1 ? 0 : tap - khh * KW);
-    seg = rfl(seg);
+    cbase = rfl(s1 ? pick(isa1, cs, cs - C1a) : pick(isa0, cur_c, cur_c - C0a));
+    kh = rfl(s1 ? cs : cur_kh);
+    kw = rfl(s1 ? 0 : cur_kw);
+    seg = rfl(s1 ? 1 : 0);
   }
+  // Both segment offsets are always computed and chosen with arithmetic
+  // selects, so the DMA sequence stays free of divergent branches.
   __device__ __forceinline__ int off(int i, int) const {
     int ih = ihb[i] + kh, iw = iwb[i] + kw;
     const bool ok0 = (pbase[i] >= 0) & ((unsigned)ih < (unsigned)Hv) & ((unsigned)iw < (unsigned)Wv);
@@ -629,7 +644,7 @@ struct ConvDma {
     const int o0 = ((pbase[i] + ih * W + iw) * ld + cbase + cch[i]) * 2;
     const bool ok1 = (mrow[i] < M) & (kh + cch[i] < C1);
     const int o1 = (mrow[i] * ld + cbase + cch[i]) * 2;
-    return seg ? (ok1 ? o1 : kOOB) : (ok0 ? o0 : kOOB);
+    return pick(seg == 0, pick(ok0, o0, kOOB), pick(ok1, o1, kOOB));
   }
 };
 
@@ -895,7 +910,8 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
   if (dma) {
     // GEGLU pairs value/gate blocks inside one wave: only 64-column waves
     switch (ep.act == DLM_ACT_GEGLU &&
-                    (g_forced_tile == 9 || g_forced_tile == 11 || g_forced_tile == 14 || g_forced_tile == 15)
+                    (g_forced_tile == 9 || g_forced_tile == 11 || g_forced_tile == 14 ||
+                     g_forced_tile == 15 || g_forced_tile == 18 || g_forced_tile == 20)
                 ? 0
                 : g_forced_tile) {
       case 8: return launch_dma<128, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
@@ -908,6 +924,9 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
       case 15: return launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s);
       case 16: return launch_dma<256, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
       case 17: return launch_dma<128, 128, 32, 64, 4>(ad, bd, ep, M, N, s);
+      case 18: return launch_dma<128, 128, 64, 32, 5>(ad, bd, ep, M, N, s);
+      case 19: return launch_dma<256, 128, 64, 64, 3>(ad, bd, ep, M, N, s);
+      case 20: return launch_dma<128, 64, 64, 32, 6>(ad, bd, ep, M, N, s);
       default: break;
     }
     if (g_forced_tile == 0 || ep.act == DLM_ACT_GEGLU) {
@@ -925,6 +944,10 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
           return ceil_div(M, 128) * ceil_div(N, 64) >= kCUs
                      ? launch_dma<128, 64, 64, 32, 2>(ad, bd, ep, M, N, s)
                      : launch_dma<128, 64, 64, 32, 4>(ad, bd, ep, M, N, s);
+        // convolutions with one to four 128x128 tiles per CU: 256x128 tiles
+        // (fewer operand bytes per MFMA; the im2col loader is the costlier one)
+        if (std::is_same<Desc, ConvDesc>::value && t128 >= kCUs && t128 < 4 * kCUs)
+          return launch_dma<256, 128, 64, 64, 3>(ad, bd, ep, M, N, s);
         return t128 >= kCUs ? launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s)
                             : launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
       }
@@ -1394,7 +1417,7 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
 }  // extern "C"
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 17, "tile_id must be in [0, 17]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 20, "tile_id must be in [0, 20]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }
