@@ -530,14 +530,15 @@ int dlm_attention_vt_fp16(const dlm_attention_vt_args* a, void* stream) {
                   stride_ok(a->vt_sb) && stride_ok(a->vt_sh) && a->vt_ld % 8 == 0 &&
                   a->o_sb % 4 == 0 && a->o_ss % 4 == 0 && a->o_sh % 4 == 0,
               "strides must keep 16-byte (Q/K/V^T) and 8-byte (O) alignment");
-  DLM_REQUIRE(a->Sk % 8 == 0 && a->vt_ld >= a->Sk, "Sk must be a multiple of 8 and vt_ld >= Sk");
+  const int sk8 = (a->Sk + 7) & ~7;
+  DLM_REQUIRE(a->vt_ld >= sk8, "vt_ld must cover Sk rounded up to a multiple of 8");
   DLM_REQUIRE(a->k_bytes > 0 && a->k_bytes < (1ull << 31) && a->vt_bytes > 0 &&
                   a->vt_bytes < (1ull << 31),
               "K and V^T buffers must be non-empty and smaller than 2 GiB");
   // every DMA offset must stay below 2^31: the last head's last key row
   const long long klast =
       ((a->B - 1) * a->k_sb + (a->H - 1) * a->k_sh + (long long)(a->Sk - 1) * a->k_ss + 64) * 2;
-  const long long vlast = ((a->B - 1) * a->vt_sb + (a->H - 1) * a->vt_sh + 63LL * a->vt_ld + a->Sk) * 2;
+  const long long vlast = ((a->B - 1) * a->vt_sb + (a->H - 1) * a->vt_sh + 63LL * a->vt_ld + sk8) * 2;
   DLM_REQUIRE(klast <= (long long)a->k_bytes && vlast <= (long long)a->vt_bytes,
               "K or V^T extends past its buffer size");
   return attention_vt(a, (hipStream_t)stream);

@@ -46,10 +46,12 @@ struct EpiArgs {
   int M;
   int N;
   // transposed-V output (DMA core only): columns >= vt_col0 of row m go to
-  // vt[((m / vt_tokens) * (N - vt_col0) + col - vt_col0) * vt_tokens + m % vt_tokens]
+  // vt[((m / vt_tokens) * (N - vt_col0) + col - vt_col0) * vt_ld + m % vt_tokens];
+  // positions [vt_tokens, vt_ld) of every V^T row are written with zeros
   f16* vt;
   int vt_col0;
   int vt_tokens;
+  int vt_ld;
 };
 
 // ---------------------------------------------------------------------------
@@ -698,10 +700,13 @@ __device__ __forceinline__ void epi4(const f32x16& a, int q, int row, int col, c
   }
   if (ep.vt && col >= ep.vt_col0) {
     const int smp = row / ep.vt_tokens;
-    f16* dst = ep.vt + ((size_t)smp * (ep.N - ep.vt_col0) + (col - ep.vt_col0)) * ep.vt_tokens +
-               (row - smp * ep.vt_tokens);
+    const int tok = row - smp * ep.vt_tokens;
+    f16* dst = ep.vt + ((size_t)smp * (ep.N - ep.vt_col0) + (col - ep.vt_col0)) * ep.vt_ld + tok;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) dst[(size_t)t * ep.vt_tokens] = (f16)v[t];
+    for (int t = 0; t < 4; ++t) dst[(size_t)t * ep.vt_ld] = (f16)v[t];
+    if (tok == ep.vt_tokens - 1)  // the last token also clears the row's padding
+      for (int t = 0; t < 4; ++t)
+        for (int q = 1; q < ep.vt_ld - tok; ++q) dst[(size_t)t * ep.vt_ld + q] = (f16)0.0f;
   } else if (ep.out_nchw) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) ep.y[((size_t)n * ep.N + col + t) * ep.rows_per_sample + p] = (f16)v[t];
@@ -997,6 +1002,7 @@ static EpiArgs make_epi(void* Y, int ldy, const void* bias, const void* R, int l
   ep.vt = nullptr;
   ep.vt_col0 = 0;
   ep.vt_tokens = 0;
+  ep.vt_ld = 0;
   return ep;
 }
 
@@ -1207,7 +1213,7 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
 }
 
 int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const void* bias, void* Y,
-                       int ldy, void* VT, int vt_col0, int tokens, int M, int N, int K,
+                       int ldy, void* VT, int vt_col0, int tokens, int vt_ld, int M, int N, int K,
                        void* stream) {
   if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
   DLM_REQUIRE(X && W && Y && VT, "NULL operand");
@@ -1219,6 +1225,7 @@ int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const voi
   DLM_REQUIRE(vt_col0 >= 0 && vt_col0 < N && vt_col0 % 4 == 0 && N % 4 == 0,
               "vt_col0 must be a multiple of 4 inside [0, N), N % 4 == 0");
   DLM_REQUIRE(tokens > 0 && M % tokens == 0, "M must be a whole number of samples of `tokens` rows");
+  DLM_REQUIRE(vt_ld >= tokens, "vt_ld smaller than tokens");
   DLM_REQUIRE(ldy >= vt_col0 && ldy % 4 == 0, "ldy must cover the columns before vt_col0");
   DLM_REQUIRE(((uintptr_t)Y & 7) == 0 && (!bias || ((uintptr_t)bias & 7) == 0),
               "Y and bias must be 8-byte aligned");
@@ -1228,6 +1235,7 @@ int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const voi
   ep.vt = (f16*)VT;
   ep.vt_col0 = vt_col0;
   ep.vt_tokens = tokens;
+  ep.vt_ld = vt_ld;
   return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
 }
 

@@ -312,7 +312,7 @@ UNet::T2D UNet::pack_t2d(const std::string& p, int C, int depth, void* stream) {
     k.bff1 = b1;
     k.wff2 = copy_of(b + "ff.net.2.weight", {C, 4 * C}, stream);
     k.bff2 = copy_of(b + "ff.net.2.bias", {C}, stream);
-    k.kv_off = kv_total_;
+    k.kv_off = kv_total_ / 2;  // row offset of this block's K (and, past all K rows, its V)
     kv_total_ += 2 * C;
     t.blocks.push_back(k);
   }
@@ -415,7 +415,8 @@ void UNet::pack_all(void* stream) {
           const Src& sv = src(prefixes[bi] + "to_v.weight", {C, c.cross_dim});
           const size_t row = (size_t)c.cross_dim * kH;
           DLM_CALL(dlm_memcpy_async(w + (size_t)k.kv_off * row, sk.ptr, (size_t)C * row, 2, stream));
-          DLM_CALL(dlm_memcpy_async(w + (size_t)(k.kv_off + C) * row, sv.ptr, (size_t)C * row, 2, stream));
+          DLM_CALL(dlm_memcpy_async(w + (size_t)(kv_total_ / 2 + k.kv_off) * row, sv.ptr,
+                                    (size_t)C * row, 2, stream));
           ++bi;
         }
       }
@@ -562,7 +563,7 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
   }
 }
 
-void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len, void* stream) {
+void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream) {
   const int C = t.C;
   const int M = B * HW;
   const int heads = C / 64;
@@ -585,8 +586,8 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len
     LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
     // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
     LAUNCH(kLinear, 2.0 * M * 3 * C * C, 0.0,
-           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, M, 3 * C, C,
-                              stream));
+           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, HW, M, 3 * C,
+                              C, stream));
     {
       dlm_attention_vt_args a{};
       const char* base = static_cast<const char*>(qkv);
@@ -622,17 +623,20 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len
          dlm_linear_fp16(n, C, k.wq2, C, nullptr, nullptr, 0, qkv, C, M, C, C, 1.0f, 0.0f,
                              DLM_ACT_NONE, stream));
     {
-      dlm_attention_args a{};
-      const char* kvb = static_cast<const char*>(kv);
+      const int kv_half = kv_total_ / 2;
+      dlm_attention_vt_args a{};
       a.q = qkv;
       a.q_sb = (long long)HW * C;
       a.q_ss = C;
       a.q_sh = 64;
-      a.k = kvb + (size_t)k.kv_off * kH;
-      a.v = kvb + (size_t)(k.kv_off + C) * kH;
-      a.k_sb = a.v_sb = (long long)ctx_len * kv_total_;
-      a.k_ss = a.v_ss = kv_total_;
-      a.k_sh = a.v_sh = 64;
+      a.k = static_cast<const char*>(kv.k) + (size_t)k.kv_off * kH;
+      a.k_sb = (long long)ctx_len * kv_half;
+      a.k_ss = kv_half;
+      a.k_sh = 64;
+      a.vt = static_cast<const char*>(kv.vt) + (size_t)k.kv_off * kv.ld * kH;
+      a.vt_sb = (long long)kv_half * kv.ld;
+      a.vt_sh = 64LL * kv.ld;
+      a.vt_ld = kv.ld;
       a.o = o;
       a.o_sb = (long long)HW * C;
       a.o_ss = C;
@@ -641,10 +645,11 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len
       a.H = heads;
       a.Sq = HW;
       a.Sk = ctx_len;
-      a.Dh = 64;
       a.scale = scale;
+      a.k_bytes = ((size_t)B * ctx_len * kv_half - k.kv_off) * kH;
+      a.vt_bytes = ((size_t)B * kv_half - k.kv_off) * kv.ld * kH;
       LAUNCH(kAttention, 4.0 * B * heads * (double)HW * ctx_len * 64, 0.0,
-             dlm_attention_strided_fp16(&a, stream));
+             dlm_attention_vt_fp16(&a, stream));
     }
     LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
          dlm_linear_fp16(o, C, k.wo2, C, k.bo2, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
@@ -701,11 +706,14 @@ void UNet::forward(int B, int H, int W, const void* latent, const float* d_times
   void* tproj = P((size_t)B * tproj_total_);
   LAUNCH(kOther, 0.0, 0.0, dlm_linear_small_fp16(temb, T, tproj_w_, tproj_b_, tproj, tproj_total_, B, tproj_total_, T,
                                  1, DLM_ACT_NONE, 0, stream));
-  // ---- cross-attention K/V of every transformer block: [B*ctx, kv_total]
-  void* kv = P((size_t)B * ctx_len * kv_total_);
+  // ---- cross-attention K/V of every transformer block, one GEMM: K as
+  // [B*ctx, sumC] row-major, V transposed as [B, sumC, ctx_pad] (zero padded)
+  const int kv_half = kv_total_ / 2;
+  const int ctx_pad = (ctx_len + 7) & ~7;
+  CrossKV ckv{P((size_t)B * ctx_len * kv_half), P((size_t)B * kv_half * ctx_pad), ctx_pad};
   LAUNCH(kLinear, 2.0 * B * ctx_len * kv_total_ * c.cross_dim, 0.0,
-         dlm_linear_fp16(ehs, c.cross_dim, kv_w_, c.cross_dim, nullptr, nullptr, 0, kv, kv_total_,
-                           B * ctx_len, kv_total_, c.cross_dim, 1.0f, 0.0f, DLM_ACT_NONE, stream));
+         dlm_linear_vt_fp16(ehs, c.cross_dim, kv_w_, c.cross_dim, nullptr, ckv.k, kv_half, ckv.vt,
+                            kv_half, ctx_len, ctx_pad, B * ctx_len, kv_total_, c.cross_dim, stream));
 
   size_t ri = 0, ai = 0;
   std::vector<std::pair<void*, int>> skips;
@@ -736,7 +744,7 @@ void UNet::forward(int B, int H, int W, const void* latent, const float* d_times
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW1 * C1);
     resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H1, W1, tproj, stream);
-    t2d(t2d_[ai++], o, B, HW1, kv, ctx_len, stream);
+    t2d(t2d_[ai++], o, B, HW1, ckv, ctx_len, stream);
     skips.push_back({o, C1});
     cur = o;
     curC = C1;
@@ -752,7 +760,7 @@ void UNet::forward(int B, int H, int W, const void* latent, const float* d_times
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW2 * C2);
     resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H2, W2, tproj, stream);
-    t2d(t2d_[ai++], o, B, HW2, kv, ctx_len, stream);
+    t2d(t2d_[ai++], o, B, HW2, ckv, ctx_len, stream);
     skips.push_back({o, C2});
     cur = o;
     curC = C2;
@@ -762,7 +770,7 @@ void UNet::forward(int B, int H, int W, const void* latent, const float* d_times
   {
     void* m0 = P((size_t)B * HW2 * C2);
     resnet(res_[ri++], cur, C2, nullptr, 0, m0, B, H2, W2, tproj, stream);
-    t2d(t2d_[ai++], m0, B, HW2, kv, ctx_len, stream);
+    t2d(t2d_[ai++], m0, B, HW2, ckv, ctx_len, stream);
     void* m1 = P((size_t)B * HW2 * C2);
     resnet(res_[ri++], m0, C2, nullptr, 0, m1, B, H2, W2, tproj, stream);
     cur = m1;
@@ -779,7 +787,7 @@ void UNet::forward(int B, int H, int W, const void* latent, const float* d_times
       skips.pop_back();
       void* o = P((size_t)B * HWu * C);
       resnet(res_[ri++], cur, curC, sk.first, sk.second, o, B, Hh, Ww, tproj, stream);
-      if (depth[u] > 0) t2d(t2d_[ai++], o, B, HWu, kv, ctx_len, stream);
+      if (depth[u] > 0) t2d(t2d_[ai++], o, B, HWu, ckv, ctx_len, stream);
       cur = o;
       curC = C;
     }

@@ -136,7 +136,13 @@ class UNet {
   // forward pieces
   void resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out, int B,
               int H, int W, const void* tproj, void* stream);
-  void t2d(const T2D& t, void* x, int B, int HW, const void* kv, int ctx_len, void* stream);
+  // every block's cross-attention K ([B*ctx, sumC]) and V^T ([B, sumC, ld])
+  struct CrossKV {
+    void* k;
+    void* vt;
+    int ld;
+  };
+  void t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream);
   void gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, const void* b, void* out,
           int B, int HW, float eps, bool silu, void* stream);
   void conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, void* out, int Co, int B,

@@ -274,20 +274,22 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias=None, residual=None, act=ACT_N
     return out
 
 
-def linear_vt(x: torch.Tensor, w: torch.Tensor, vt_col0: int, tokens: int, bias=None):
+def linear_vt(x: torch.Tensor, w: torch.Tensor, vt_col0: int, tokens: int, bias=None, vt_ld=None):
     """y = x @ w.T for columns [0, vt_col0) as [M, vt_col0], and the remaining
-    columns transposed per sample as vt [M // tokens, N - vt_col0, tokens]."""
+    columns transposed per sample as vt [M // tokens, N - vt_col0, vt_ld]
+    (vt_ld >= tokens; positions past `tokens` are zero)."""
+    vt_ld = vt_ld or tokens
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K or M % tokens != 0:
         raise ValueError("shape mismatch")
     y = torch.empty(M, vt_col0, dtype=torch.float16, device=x.device)
-    vt = torch.empty(M // tokens, N - vt_col0, tokens, dtype=torch.float16, device=x.device)
+    vt = torch.empty(M // tokens, N - vt_col0, vt_ld, dtype=torch.float16, device=x.device)
     _need(x, M * K, "x")
     _need(w, N * K, "w")
     _need(bias, N, "bias", optional=True)
     call("dlm_linear_vt_fp16", _p(x), K, _p(w), K, _p(bias), _p(y), vt_col0, _p(vt), vt_col0,
-         tokens, M, N, K, stream_handle())
+         tokens, vt_ld, M, N, K, stream_handle())
     return y, vt
 
 
@@ -439,7 +441,7 @@ def attention_vt(q, k, vt, o, *, B, H, Sq, Sk, q_strides, k_strides, vt_strides,
     def _span(strides, S):
         sb, ss, sh = strides
         return (B - 1) * sb + (S - 1) * ss + (H - 1) * sh + 64
-    vspan = (B - 1) * vt_strides[0] + (H - 1) * vt_strides[1] + 63 * vt_ld + Sk
+    vspan = (B - 1) * vt_strides[0] + (H - 1) * vt_strides[1] + 63 * vt_ld + ((Sk + 7) & ~7)
     for t, span, nm in ((q, _span(q_strides, Sq), "q"), (k, _span(k_strides, Sk), "k"),
                         (vt, vspan, "vt"), (o, _span(o_strides, Sq), "o")):
         if t.storage_offset() + span > t.untyped_storage().nbytes() // 2:

@@ -172,14 +172,15 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
 
 /* Linear with a transposed tail: Y = X W^T for columns [0, vt_col0) (row
  * stride ldy) and, for columns n >= vt_col0, the transpose per sample:
- * VT[(m / tokens) * (N - vt_col0) + n - vt_col0][m % tokens] (row stride
- * `tokens`).  Fed with the fused QKV weight [3C, C] and vt_col0 = 2C it
- * writes Q|K as [M, 2C] and V^T as [B, C, tokens] = [B, H, 64, tokens], the
- * layout dlm_attention_vt_fp16 reads.  No counterpart in the reference,
- * which splits heads with separate kernels (k_split_heads,
+ * VT[(m / tokens) * (N - vt_col0) + n - vt_col0][m % tokens] with row stride
+ * vt_ld >= tokens; entries [tokens, vt_ld) of every V^T row are set to 0.
+ * Fed with the fused QKV weight [3C, C] and vt_col0 = 2C it writes Q|K as
+ * [M, 2C] and V^T as [B, C, vt_ld] = [B, H, 64, vt_ld], the layout
+ * dlm_attention_vt_fp16 reads.  No counterpart in the reference, which
+ * splits heads with separate kernels (k_split_heads,
  * src/infer/unet.cu:153-278). */
 int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const void* bias, void* Y,
-                       int ldy, void* VT, int vt_col0, int tokens, int M, int N, int K,
+                       int ldy, void* VT, int vt_col0, int tokens, int vt_ld, int M, int N, int K,
                        void* stream);
 
 /* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
@@ -248,8 +249,10 @@ typedef struct dlm_attention_args {
 int dlm_attention_strided_fp16(const dlm_attention_args* args, void* stream);
 
 /* Flash attention with V supplied transposed: element (b, h, d, key) of V^T
- * is at vt[b*vt_sb + h*vt_sh + d*vt_ld + key] (vt_ld >= Sk, multiple of 8).
- * Q, K, O as in dlm_attention_args; Dh = 64; Sk % 8 == 0.  k_bytes and
+ * is at vt[b*vt_sb + h*vt_sh + d*vt_ld + key] (vt_ld a multiple of 8 and at
+ * least Sk rounded up to 8; keys [Sk, that) must hold finite values, e.g.
+ * the zeros dlm_linear_vt_fp16 writes).  Q, K, O as in dlm_attention_args;
+ * Dh = 64.  k_bytes and
  * vt_bytes bound the K and V^T allocations (each < 2 GiB): reads past them
  * return zero.  The UNet's QKV projection writes V^T directly (see
  * dlm_linear_vt_fp16), so self-attention needs no LDS transpose.

@@ -230,7 +230,8 @@ def test_attention_strided_fused_qkv(gpu):
 
 
 @pytest.mark.parametrize("B,H,Sq,Sk", [(1, 1, 32, 64), (1, 2, 300, 136), (2, 10, 4096, 4096),
-                                       (2, 20, 1024, 1024), (1, 3, 1000, 8)])
+                                       (2, 20, 1024, 1024), (1, 3, 1000, 8), (2, 10, 4096, 77),
+                                       (2, 20, 1024, 77), (1, 2, 64, 5)])
 def test_attention_vt(gpu, B, H, Sq, Sk):
     """Flash attention over V^T [B, H, 64, Sk] with Q/K read from a fused
     [B, S, 2C] buffer; partial last key tiles, Sq not a multiple of the
@@ -241,24 +242,29 @@ def test_attention_vt(gpu, B, H, Sq, Sk):
     q, k, v = randn((B, H, Sq, Dh), 120), randn((B, H, Sk, Dh), 121), randn((B, H, Sk, Dh), 122)
     dq = to_gpu(q.permute(0, 2, 1, 3).reshape(B, Sq, C))
     dk = to_gpu(k.permute(0, 2, 1, 3).reshape(B, Sk, C))
-    vt = to_gpu(v.transpose(2, 3).contiguous())  # [B, H, 64, Sk]
+    ld = (Sk + 7) // 8 * 8
+    vt = torch.zeros(B, H, Dh, ld, dtype=torch.float16, device=gpu)  # [B, H, 64, ld], zero padded
+    vt[..., :Sk] = to_gpu(v.transpose(2, 3).contiguous())
     o = torch.empty(B, Sq, C, dtype=torch.float16, device=gpu)
     ops.attention_vt(dq, dk, vt, o, B=B, H=H, Sq=Sq, Sk=Sk, q_strides=(Sq * C, C, Dh),
-                     k_strides=(Sk * C, C, Dh), vt_strides=(H * Dh * Sk, Dh * Sk), vt_ld=Sk,
+                     k_strides=(Sk * C, C, Dh), vt_strides=(H * Dh * ld, Dh * ld), vt_ld=ld,
                      o_strides=(Sq * C, C, Dh), scale=0.125)
     ref = torch.cat([R.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], 0.125) for b in range(B)])
     assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), "attention_vt")
 
 
-@pytest.mark.parametrize("B,S,C", [(2, 1024, 1280), (2, 64, 128), (3, 40, 192)])
-def test_linear_vt(gpu, B, S, C):
-    """Fused QKV projection writing Q|K row-major and V transposed per sample."""
-    announce(f"linear_vt B={B} S={S} C={C}")
+@pytest.mark.parametrize("B,S,C,ld", [(2, 1024, 1280, 1024), (2, 64, 128, 64), (3, 40, 192, 40),
+                                      (2, 77, 640, 80)])
+def test_linear_vt(gpu, B, S, C, ld):
+    """Fused QKV projection writing Q|K row-major and V transposed per sample,
+    V^T rows padded to `ld` with zeros."""
+    announce(f"linear_vt B={B} S={S} C={C} ld={ld}")
     x, w, b = randn((B * S, C), 130), randn((3 * C, C), 131, 0.05), randn((3 * C,), 132, 0.1)
-    y, vt = ops.linear_vt(to_gpu(x), to_gpu(w), 2 * C, S, bias=to_gpu(b))
+    y, vt = ops.linear_vt(to_gpu(x), to_gpu(w), 2 * C, S, bias=to_gpu(b), vt_ld=ld)
     ref = R.linear(x, w, b)
     assert_close(y, ref[:, :2 * C], "linear_vt y")
-    assert_close(vt, ref[:, 2 * C:].reshape(B, S, C).transpose(1, 2), "linear_vt vt")
+    assert_close(vt[:, :, :S], ref[:, 2 * C:].reshape(B, S, C).transpose(1, 2), "linear_vt vt")
+    assert bool((vt[:, :, S:] == 0).all())
 
 
 # ------------------------------------------------------------ small ops ---
