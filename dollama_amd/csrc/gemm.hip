@@ -1073,6 +1073,23 @@ __global__ void conv_weight_pack_kernel(const f16* __restrict__ w, f16* __restri
   }
 }
 
+// out[co*ld + col0 + tap*Cin_pad + ci] += w[co][ci][tap] for ci < Cin (fp32
+// add, fp16 round); the zero padding ci >= Cin is left untouched.
+__global__ void conv_weight_pack_add_kernel(const f16* __restrict__ w, f16* __restrict__ out,
+                                            int Cout, int Cin, int taps, int Cin_pad, int ld,
+                                            int col0) {
+  const long long total = (long long)Cout * taps * Cin;
+  for (long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int ci = (int)(idx % Cin);
+    const long long r = idx / Cin;
+    const int tap = (int)(r % taps);
+    const int co = (int)(r / taps);
+    f16* o = out + (size_t)co * ld + col0 + (size_t)tap * Cin_pad + ci;
+    *o = (f16)((float)*o + (float)w[((size_t)co * Cin + ci) * taps + tap]);
+  }
+}
+
 // GEGLU interleave in 32-row block pairs: packed row 64p+s <- value row
 // 32p+s (s<32) or gate row d+32p+s-32 (s>=32).
 __global__ void geglu_pack_kernel(const f16* __restrict__ w, const f16* __restrict__ b,
@@ -1114,6 +1131,16 @@ int nhwc_to_nchw(const void* in, void* out, int N, int C, int HW, int C_pad, hip
   dim3 grid((HW + 31) / 32, (C + 31) / 32, N);
   hipLaunchKernelGGL(nhwc_to_nchw_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
                      HW, C_pad);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int conv_weight_pack_add(const void* w, void* out, int Cout, int Cin, int KH, int KW, int Cin_pad,
+                         int ld, int col0, hipStream_t s) {
+  const long long total = (long long)Cout * KH * KW * Cin;
+  const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(conv_weight_pack_add_kernel, dim3(blocks), dim3(256), 0, s, (const f16*)w,
+                     (f16*)out, Cout, Cin, KH * KW, Cin_pad, ld, col0);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -1303,6 +1330,16 @@ int dlm_conv_weight_pack_fp16(const void* w, void* out, int Cout, int Cin, int K
   DLM_REQUIRE(Cin_pad >= Cin, "Cin_pad < Cin");
   DLM_REQUIRE(ld_out >= col0 + KH * KW * Cin_pad, "ld_out too small");
   return conv_weight_pack(w, out, Cout, Cin, KH, KW, Cin_pad, ld_out, col0, (hipStream_t)stream);
+}
+
+int dlm_conv_weight_pack_add_fp16(const void* w, void* out, int Cout, int Cin, int KH, int KW,
+                                  int Cin_pad, int ld_out, int col0, void* stream) {
+  if (Cout <= 0 || Cin <= 0 || KH <= 0 || KW <= 0) return DLM_OK;
+  DLM_REQUIRE(w && out, "NULL pointer");
+  DLM_REQUIRE(Cin_pad >= Cin, "Cin_pad < Cin");
+  DLM_REQUIRE(ld_out >= col0 + KH * KW * Cin_pad, "ld_out too small");
+  return conv_weight_pack_add(w, out, Cout, Cin, KH, KW, Cin_pad, ld_out, col0,
+                              (hipStream_t)stream);
 }
 
 int dlm_nchw_to_nhwc_fp16(const void* in, void* out, int N, int C, int HW, int C_pad,

@@ -10,6 +10,7 @@
 
 #include "check.hpp"
 #include "device_arena.hpp"
+#include "lora.hpp"
 #include "pipeline.hpp"
 #include "safetensors.hpp"
 #include "scheduler.hpp"
@@ -153,6 +154,78 @@ int dlm_unet_load_safetensors(void* handle, const char* path, void* stream) {
       u->set_weight(s.name, static_cast<char*>(dev) + st.offset(s.name), st.shape(s.name));
     }
     u->prepare(stream);
+  });
+}
+
+int dlm_unet_apply_lora(void* handle, const char* base_key, const void* A, const void* B, int rank,
+                        int in_flat, int out_dim, float scale, void* stream) {
+  return guarded([&] {
+    if (!handle || !base_key || !A || !B) throw std::invalid_argument("NULL argument");
+    static_cast<UNet*>(handle)->apply_lora(base_key, A, B, rank, in_flat, out_dim, scale, stream);
+  });
+}
+
+static void fill_counts(int* counts, const LoraReport& r) {
+  if (!counts) return;
+  counts[0] = (int)r.modules;
+  counts[1] = (int)r.te_skipped;
+  counts[2] = (int)r.other_keys;
+  counts[3] = (int)r.incomplete;
+}
+
+int dlm_unet_load_lora(void* handle, const char* path, float strength, int* counts, void* stream) {
+  return guarded([&] {
+    if (!handle || !path) throw std::invalid_argument("NULL argument");
+    UNet* u = static_cast<UNet*>(handle);
+    SafeTensors st(path);
+    LoraReport rep;
+    std::vector<LoraModule> mods = load_lora_modules(unet_weight_specs(u->config()), st, strength, &rep);
+    for (const LoraModule& m : mods) {
+      void* dev = nullptr;
+      const size_t na = m.a_fp16.size(), nb = m.b_fp16.size();
+      DLM_CALL(dlm_malloc(&dev, (na + nb) * 2));
+      std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
+      DLM_CALL(dlm_memcpy(dev, m.a_fp16.data(), na * 2, 0));
+      DLM_CALL(dlm_memcpy(static_cast<uint16_t*>(dev) + na, m.b_fp16.data(), nb * 2, 0));
+      u->apply_lora(m.base_key, dev, static_cast<uint16_t*>(dev) + na, m.rank, m.in_flat, m.out_dim,
+                    m.scale, stream);
+    }
+    fill_counts(counts, rep);
+  });
+}
+
+int dlm_unet_clear_loras(void* handle, void* stream) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<UNet*>(handle)->clear_loras(stream);
+  });
+}
+
+int dlm_lora_scan(const dlm_unet_config* cfg, const char* path, float strength, int* counts,
+                  dlm_lora_module_fn fn, void* user) {
+  return guarded([&] {
+    if (!cfg || !path) throw std::invalid_argument("NULL argument");
+    SafeTensors st(path);
+    LoraReport rep;
+    const std::vector<LoraModule> mods =
+        load_lora_modules(unet_weight_specs(to_cfg(cfg)), st, strength, &rep);
+    fill_counts(counts, rep);
+    if (fn)
+      for (const LoraModule& m : mods) fn(m.base_key.c_str(), m.rank, m.in_flat, m.out_dim, m.scale, user);
+  });
+}
+
+int dlm_unet_read_weight(void* handle, const char* name, void* host_out, size_t bytes, void* stream) {
+  return guarded([&] {
+    if (!handle || !name || !host_out) throw std::invalid_argument("NULL argument");
+    static_cast<UNet*>(handle)->read_weight(name, host_out, bytes, stream);
+  });
+}
+
+int dlm_f32_to_f16(const float* in, uint16_t* out, size_t n) {
+  return guarded([&] {
+    if ((!in || !out) && n) throw std::invalid_argument("NULL argument");
+    for (size_t i = 0; i < n; ++i) out[i] = f32_to_f16_rne(in[i]);
   });
 }
 

@@ -155,8 +155,93 @@ UNet::UNet(const UNetConfig& cfg) : cfg_(cfg) {
 }
 
 UNet::~UNet() {
+  for (Backup& b : backups_) (void)dlm_free(b.copy);
   if (packed_) (void)dlm_free(packed_);
   for (void* e : prof_events_) (void)dlm_event_destroy(e);
+}
+
+// ---------------------------------------------------------------------------
+// Runtime LoRA (reference src/infer/unet.cu:373-458): W += scale * (B @ A) on
+// the resident weights.  delta = scale * (B @ A) is formed in fp16 by the
+// MFMA GEMM (fp32 accumulate), packed exactly like the weight it patches
+// (plain rows, GEGLU interleave or the per-tap conv layout) and added
+// element-wise (fp32 add, fp16 round), so W' = f16(W + f16(delta)) as in the
+// reference.  The packed region is copied aside before its first patch;
+// clear_loras() copies every saved region back (bit-exact revert).
+// ---------------------------------------------------------------------------
+void UNet::apply_lora(const std::string& key, const void* dA, const void* dB, int rank,
+                      int in_flat, int out_dim, float scale, void* stream) {
+  if (!prepared()) throw std::logic_error("UNet::apply_lora before prepare()");
+  auto it = placed_.find(key);
+  if (it == placed_.end()) throw std::invalid_argument("lora: '" + key + "' is not a UNet weight");
+  const Placement& pl = it->second;
+  const size_t n = (size_t)out_dim * in_flat;
+  size_t wn = pl.elems;
+  if (pl.kind == Placement::kConv) wn = (size_t)pl.Co * pl.Ci * pl.k * pl.k;
+  if (rank <= 0 || n != wn)
+    throw std::invalid_argument("lora: '" + key + "' delta shape does not match the weight");
+  if (!patched_.count(key)) {  // save the packed region once
+    Backup bk;
+    bk.dst = pl.dst;
+    bk.bytes = pl.elems * kH;
+    DLM_CALL(dlm_malloc(&bk.copy, bk.bytes));
+    DLM_CALL(dlm_memcpy_async(bk.copy, bk.dst, bk.bytes, 2, stream));
+    backups_.push_back(bk);
+    patched_.insert(key);
+  }
+  DeviceArenaScope sc(DeviceArenaId::UNet);
+  void* delta = sc.alloc<uint16_t>(n);
+  DLM_CALL(dlm_gemm_fp16(dB, dA, delta, out_dim, in_flat, rank, scale, 0.0f, 0, 0, stream));
+  if (pl.kind == Placement::kCopy) {
+    DLM_CALL(dlm_add_fp16(pl.dst, delta, pl.dst, (int)n, stream));
+  } else if (pl.kind == Placement::kGeglu) {
+    void* packed = sc.alloc<uint16_t>(n);
+    DLM_CALL(dlm_geglu_pack_fp16(delta, nullptr, packed, nullptr, pl.Co / 2, pl.Ci, stream));
+    DLM_CALL(dlm_add_fp16(pl.dst, packed, pl.dst, (int)n, stream));
+  } else {
+    DLM_CALL(dlm_conv_weight_pack_add_fp16(delta, pl.dst, pl.Co, pl.Ci, pl.k, pl.k, pl.cin_pad,
+                                           pl.ld, pl.col0, stream));
+  }
+  DLM_CALL(dlm_stream_synchronize(stream));  // the arena scope ends here
+}
+
+void UNet::clear_loras(void* stream) {
+  for (auto it = backups_.rbegin(); it != backups_.rend(); ++it)
+    DLM_CALL(dlm_memcpy_async(it->dst, it->copy, it->bytes, 2, stream));
+  DLM_CALL(dlm_stream_synchronize(stream));
+  for (Backup& b : backups_) dlm_free(b.copy);
+  backups_.clear();
+  patched_.clear();
+}
+
+void UNet::read_weight(const std::string& key, void* host, size_t bytes, void* stream) const {
+  if (!prepared()) throw std::logic_error("UNet::read_weight before prepare()");
+  auto it = placed_.find(key);
+  if (it == placed_.end()) throw std::invalid_argument("'" + key + "' is not a resident weight");
+  const Placement& pl = it->second;
+  const size_t n = pl.kind == Placement::kConv ? (size_t)pl.Co * pl.Ci * pl.k * pl.k : pl.elems;
+  if (bytes != n * kH) throw std::invalid_argument("'" + key + "' holds " + std::to_string(n * kH) + " bytes");
+  std::vector<uint16_t> raw(pl.elems);
+  DLM_CALL(dlm_memcpy_async(raw.data(), pl.dst, pl.elems * kH, 1, stream));
+  DLM_CALL(dlm_stream_synchronize(stream));
+  uint16_t* out = static_cast<uint16_t*>(host);
+  if (pl.kind == Placement::kCopy) {
+    std::copy(raw.begin(), raw.end(), out);
+  } else if (pl.kind == Placement::kGeglu) {  // packed row 64q+s <- value 32q+s | gate d+32q+s-32
+    const int d = pl.Co / 2, K = pl.Ci;
+    for (int r = 0; r < pl.Co; ++r) {
+      const int q = r / 64, s = r % 64;
+      const int src = s < 32 ? 32 * q + s : d + 32 * q + (s - 32);
+      std::copy(raw.begin() + (size_t)r * K, raw.begin() + (size_t)(r + 1) * K, out + (size_t)src * K);
+    }
+  } else {  // packed [co][col0 + tap * cin_pad + ci] <- [co][ci][tap]
+    const int taps = pl.k * pl.k;
+    for (int co = 0; co < pl.Co; ++co)
+      for (int ci = 0; ci < pl.Ci; ++ci)
+        for (int t = 0; t < taps; ++t)
+          out[((size_t)co * pl.Ci + ci) * taps + t] =
+              raw[(size_t)co * pl.ld + pl.col0 + (size_t)t * pl.cin_pad + ci];
+  }
 }
 
 void UNet::set_profiling(bool on) { prof_on_ = on; }
@@ -221,8 +306,34 @@ const void* UNet::copy_of(const std::string& name, const Shape& shape, void* str
   size_t n = 1;
   for (int64_t d : shape) n *= (size_t)d;
   void* dst = take(n);
-  if (!sizing_) DLM_CALL(dlm_memcpy_async(dst, s.ptr, n * kH, 2, stream));
+  if (!sizing_) {
+    DLM_CALL(dlm_memcpy_async(dst, s.ptr, n * kH, 2, stream));
+    place_copy(name, dst, n);
+  }
   return dst;
+}
+
+void UNet::place_copy(const std::string& name, void* dst, size_t n) {
+  Placement pl;
+  pl.kind = Placement::kCopy;
+  pl.dst = static_cast<char*>(dst);
+  pl.elems = n;
+  placed_[name] = pl;
+}
+
+void UNet::place_conv(const std::string& name, void* dst, int Co, int Ci, int k, int cin_pad,
+                      int ld, int col0) {
+  Placement pl;
+  pl.kind = Placement::kConv;
+  pl.dst = static_cast<char*>(dst);
+  pl.elems = (size_t)Co * ld;  // the whole packed rows (shared with a second K segment)
+  pl.Co = Co;
+  pl.Ci = Ci;
+  pl.k = k;
+  pl.cin_pad = cin_pad;
+  pl.ld = ld;
+  pl.col0 = col0;
+  placed_[name] = pl;
 }
 
 UNet::Conv UNet::pack_conv(const std::string& p, int Co, int Ci, int k, int cin_pad, void* stream) {
@@ -230,7 +341,10 @@ UNet::Conv UNet::pack_conv(const std::string& p, int Co, int Ci, int k, int cin_
   c.ldw = k * k * cin_pad;
   void* w = take((size_t)Co * c.ldw);
   const Src& s = src(p + "weight", {Co, Ci, k, k});
-  if (!sizing_) DLM_CALL(dlm_conv_weight_pack_fp16(s.ptr, w, Co, Ci, k, k, cin_pad, c.ldw, 0, stream));
+  if (!sizing_) {
+    DLM_CALL(dlm_conv_weight_pack_fp16(s.ptr, w, Co, Ci, k, k, cin_pad, c.ldw, 0, stream));
+    place_conv(p + "weight", w, Co, Ci, k, cin_pad, c.ldw, 0);
+  }
   c.w = w;
   c.b = copy_of(p + "bias", {Co}, stream);
   return c;
@@ -245,7 +359,10 @@ UNet::Resnet UNet::pack_resnet(const std::string& p, int Ci, int Co, void* strea
   r.n1b = copy_of(p + "norm1.bias", {Ci}, stream);
   void* c1 = take((size_t)Co * 9 * Ci);
   const Src& s1 = src(p + "conv1.weight", {Co, Ci, 3, 3});
-  if (!sizing_) DLM_CALL(dlm_conv_weight_pack_fp16(s1.ptr, c1, Co, Ci, 3, 3, Ci, 9 * Ci, 0, stream));
+  if (!sizing_) {
+    DLM_CALL(dlm_conv_weight_pack_fp16(s1.ptr, c1, Co, Ci, 3, 3, Ci, 9 * Ci, 0, stream));
+    place_conv(p + "conv1.weight", c1, Co, Ci, 3, Ci, 9 * Ci, 0);
+  }
   r.c1w = c1;
   r.c1b = copy_of(p + "conv1.bias", {Co}, stream);
   r.n2g = copy_of(p + "norm2.weight", {Co}, stream);
@@ -254,12 +371,17 @@ UNet::Resnet UNet::pack_resnet(const std::string& p, int Ci, int Co, void* strea
   r.c2_ldw = 9 * Co + (r.shortcut ? Ci : 0);
   void* c2 = take((size_t)Co * r.c2_ldw);
   const Src& s2 = src(p + "conv2.weight", {Co, Co, 3, 3});
-  if (!sizing_) DLM_CALL(dlm_conv_weight_pack_fp16(s2.ptr, c2, Co, Co, 3, 3, Co, r.c2_ldw, 0, stream));
+  if (!sizing_) {
+    DLM_CALL(dlm_conv_weight_pack_fp16(s2.ptr, c2, Co, Co, 3, 3, Co, r.c2_ldw, 0, stream));
+    place_conv(p + "conv2.weight", c2, Co, Co, 3, Co, r.c2_ldw, 0);
+  }
   r.c2w = c2;
   if (r.shortcut) {
     const Src& ss = src(p + "conv_shortcut.weight", {Co, Ci, 1, 1});
-    if (!sizing_)
+    if (!sizing_) {
       DLM_CALL(dlm_conv_weight_pack_fp16(ss.ptr, c2, Co, Ci, 1, 1, Ci, r.c2_ldw, 9 * Co, stream));
+      place_conv(p + "conv_shortcut.weight", c2, Co, Ci, 1, Ci, r.c2_ldw, 9 * Co);
+    }
     void* b = take(Co);
     const Src& b2 = src(p + "conv2.bias", {Co});
     const Src& bs = src(p + "conv_shortcut.bias", {Co});
@@ -292,8 +414,10 @@ UNet::T2D UNet::pack_t2d(const std::string& p, int C, int depth, void* stream) {
     int i = 0;
     for (const char* n : {"to_q", "to_k", "to_v"}) {
       const Src& s = src(b + "attn1." + n + ".weight", {C, C});
-      if (!sizing_)
+      if (!sizing_) {
         DLM_CALL(dlm_memcpy_async(qkv + (size_t)i * C * C * kH, s.ptr, (size_t)C * C * kH, 2, stream));
+        place_copy(b + "attn1." + n + ".weight", qkv + (size_t)i * C * C * kH, (size_t)C * C);
+      }
       ++i;
     }
     k.wqkv = qkv;
@@ -302,12 +426,21 @@ UNet::T2D UNet::pack_t2d(const std::string& p, int C, int depth, void* stream) {
     k.wq2 = copy_of(b + "attn2.to_q.weight", {C, C}, stream);
     k.wo2 = copy_of(b + "attn2.to_out.0.weight", {C, C}, stream);
     k.bo2 = copy_of(b + "attn2.to_out.0.bias", {C}, stream);
-    // GEGLU projection in the 16-row interleave
+    // GEGLU projection in the 32-row value/gate interleave
     void* w1 = take((size_t)8 * C * C);
     void* b1 = take((size_t)8 * C);
     const Src& sw = src(b + "ff.net.0.proj.weight", {8 * C, C});
     const Src& sb = src(b + "ff.net.0.proj.bias", {8 * C});
-    if (!sizing_) DLM_CALL(dlm_geglu_pack_fp16(sw.ptr, sb.ptr, w1, b1, 4 * C, C, stream));
+    if (!sizing_) {
+      DLM_CALL(dlm_geglu_pack_fp16(sw.ptr, sb.ptr, w1, b1, 4 * C, C, stream));
+      Placement pl;
+      pl.kind = Placement::kGeglu;
+      pl.dst = static_cast<char*>(w1);
+      pl.elems = (size_t)8 * C * C;
+      pl.Co = 8 * C;
+      pl.Ci = C;
+      placed_[b + "ff.net.0.proj.weight"] = pl;
+    }
     k.wff1 = w1;
     k.bff1 = b1;
     k.wff2 = copy_of(b + "ff.net.2.weight", {C, 4 * C}, stream);
@@ -393,6 +526,7 @@ void UNet::pack_all(void* stream) {
         const Src& sw = src(p + "weight", {Co, T});
         const Src& sb = src(p + "bias", {Co});
         DLM_CALL(dlm_memcpy_async(w + (size_t)res_[i].tproj_off * T * kH, sw.ptr, (size_t)Co * T * kH, 2, stream));
+        place_copy(p + "weight", w + (size_t)res_[i].tproj_off * T * kH, (size_t)Co * T);
         DLM_CALL(dlm_memcpy_async(b + (size_t)res_[i].tproj_off * kH, sb.ptr, (size_t)Co * kH, 2, stream));
       }
     }
@@ -417,6 +551,9 @@ void UNet::pack_all(void* stream) {
           DLM_CALL(dlm_memcpy_async(w + (size_t)k.kv_off * row, sk.ptr, (size_t)C * row, 2, stream));
           DLM_CALL(dlm_memcpy_async(w + (size_t)(kv_total_ / 2 + k.kv_off) * row, sv.ptr,
                                     (size_t)C * row, 2, stream));
+          place_copy(prefixes[bi] + "to_k.weight", w + (size_t)k.kv_off * row, (size_t)C * c.cross_dim);
+          place_copy(prefixes[bi] + "to_v.weight", w + (size_t)(kv_total_ / 2 + k.kv_off) * row,
+                     (size_t)C * c.cross_dim);
           ++bi;
         }
       }
@@ -426,6 +563,11 @@ void UNet::pack_all(void* stream) {
 }
 
 void UNet::prepare(void* stream) {
+  // a re-pack starts from the registered weights: earlier LoRA state is void
+  for (Backup& b : backups_) (void)dlm_free(b.copy);
+  backups_.clear();
+  patched_.clear();
+  placed_.clear();
   // pass 1: sizes and validation
   sizing_ = true;
   pack_all(stream);

@@ -24,6 +24,7 @@
 #include <cstdint>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "dlm.h"
@@ -78,6 +79,18 @@ class UNet {
                int ctx_len, const void* text, const void* time_ids, int ids_bstride, void* out,
                void* stream);
 
+  // Runtime LoRA merge on the resident weights: W += scale * (B @ A) with
+  // device fp16 A [rank, in_flat] and B [out_dim, rank]; clear_loras() restores
+  // every patched weight bit-exactly.  Synchronises the stream.
+  void apply_lora(const std::string& key, const void* dA, const void* dB, int rank, int in_flat,
+                  int out_dim, float scale, void* stream);
+  void clear_loras(void* stream);
+  size_t lora_patched() const { return patched_.size(); }
+  // Copy the resident fp16 weight `key` back to host memory in its diffusers
+  // layout (undoing the GEGLU interleave and the per-tap conv packing);
+  // bytes must equal 2 * its element count.  Synchronises the stream.
+  void read_weight(const std::string& key, void* host, size_t bytes, void* stream) const;
+
   void set_stage_hook(UnetStageHook hook, void* user) {
     hook_ = hook;
     hook_user_ = user;
@@ -123,6 +136,25 @@ class UNet {
     const void* ptr;
     std::vector<int64_t> shape;
   };
+
+  // where each named weight lives in the packed storage (for LoRA)
+  struct Placement {
+    enum Kind { kCopy, kConv, kGeglu } kind = kCopy;
+    char* dst = nullptr;
+    size_t elems = 0;
+    int Co = 0, Ci = 0, k = 0, cin_pad = 0, ld = 0, col0 = 0;
+  };
+  struct Backup {
+    char* dst;
+    void* copy;
+    size_t bytes;
+  };
+  std::unordered_map<std::string, Placement> placed_;
+  std::vector<Backup> backups_;
+  std::unordered_set<std::string> patched_;
+  void place_copy(const std::string& name, void* dst, size_t n);
+  void place_conv(const std::string& name, void* dst, int Co, int Ci, int k, int cin_pad, int ld,
+                  int col0);
 
   // packing helpers (two passes: sizing, then filling)
   const Src& src(const std::string& name, const std::vector<int64_t>& shape) const;

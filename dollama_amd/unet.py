@@ -65,6 +65,12 @@ HOST_SIGNATURES = {
     "dlm_unet_profile_report": (I, [P, POINTER(ctypes.c_double), P]),
     "dlm_euler_schedule": (I, [I, POINTER(ctypes.c_float), POINTER(ctypes.c_float)]),
     "dlm_pipeline_denoise": (I, [P, I, ctypes.c_float, I, I, P, P, I, P, P, P]),
+    "dlm_unet_apply_lora": (I, [P, ctypes.c_char_p, P, P, I, I, I, ctypes.c_float, P]),
+    "dlm_unet_load_lora": (I, [P, ctypes.c_char_p, ctypes.c_float, POINTER(c_int), P]),
+    "dlm_unet_clear_loras": (I, [P, P]),
+    "dlm_lora_scan": (I, [P, ctypes.c_char_p, ctypes.c_float, POINTER(c_int), P, P]),
+    "dlm_unet_read_weight": (I, [P, ctypes.c_char_p, P, c_size_t, P]),
+    "dlm_f32_to_f16": (I, [P, P, c_size_t]),
     "dlm_arena_stats": (I, [I, POINTER(c_uint64)]),
     "dlm_arena_release": (I, [I]),
     "dlm_arena_reserve": (I, [I, c_size_t]),
@@ -109,6 +115,41 @@ ARENA_STAT_FIELDS = ("cuda_malloc_calls", "cuda_free_calls", "chunk_alloc_calls"
                      "total_capacity", "live_chunks", "bytes_in_use", "peak_bytes_in_use",
                      "live_request_bytes", "peak_request_bytes", "reserved_bytes")
 ARENA_UNET, ARENA_VAE, ARENA_UNET_PERSIST = 0, 1, 2
+
+
+LORA_COUNT_FIELDS = ("modules", "te_skipped", "other_keys", "incomplete")
+
+
+LORA_MODULE_FN = CFUNCTYPE(None, c_char_p, c_int, c_int, c_int, ctypes.c_float, c_void_p)
+
+
+def lora_scan(path: str, strength: float = 1.0, cfg: UNetConfig = SDXL_CONFIG):
+    """Resolve a kohya-named LoRA file against the UNet weight names of cfg
+    (host only; reference load_lora_modules, src/infer/lora.hpp:265-445).
+    Returns (counts, modules) with modules = {base_key: (rank, in_flat,
+    out_dim, scale)}.  Raises on a module that matches no weight or has
+    mismatched shapes."""
+    c = cfg.to_c()
+    v = (c_int * 4)()
+    mods = {}
+
+    def _cb(key, rank, in_flat, out_dim, scale, user):
+        mods[key.decode()] = (rank, in_flat, out_dim, scale)
+
+    fn = LORA_MODULE_FN(_cb)
+    _call("dlm_lora_scan", ctypes.byref(c), path.encode(), float(strength), v,
+          ctypes.cast(fn, c_void_p), None)
+    return dict(zip(LORA_COUNT_FIELDS, list(v))), mods
+
+
+def f32_to_f16_bits(x) -> "numpy.ndarray":
+    """fp32 -> fp16 bit patterns with round-to-nearest-even, as the LoRA
+    loader converts F32 tensors."""
+    import numpy as np
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    _call("dlm_f32_to_f16", c_void_p(a.ctypes.data), c_void_p(out.ctypes.data), a.size)
+    return out
 
 
 def arena_stats(arena_id: int) -> dict:
@@ -199,6 +240,40 @@ class UNet:
         _call("dlm_unet_forward", self._h, B, H, W, c_void_p(latent.data_ptr()),
               c_void_p(timesteps.data_ptr()), c_void_p(ehs.data_ptr()), L, c_void_p(text.data_ptr()),
               c_void_p(time_ids.data_ptr()), ids_stride, c_void_p(out.data_ptr()), _stream())
+        return out
+
+    def apply_lora(self, key: str, A: torch.Tensor, B: torch.Tensor, scale: float):
+        """W += scale * (B @ A) on the resident weight `key` (diffusers name);
+        A [rank, in(,kh,kw)] and B [out, rank(,1,1)] fp16 GPU tensors
+        (reference src/infer/unet.cuh:97-114)."""
+        for t in (A, B):
+            if not t.is_cuda or t.dtype != torch.float16 or not t.is_contiguous():
+                raise ValueError("LoRA factors must be contiguous fp16 GPU tensors")
+        rank = A.shape[0]
+        in_flat = A.numel() // max(rank, 1)
+        out_dim = B.shape[0]
+        if B.numel() != out_dim * rank:
+            raise ValueError("B does not match the rank of A")
+        _call("dlm_unet_apply_lora", self._h, key.encode(), c_void_p(A.data_ptr()),
+              c_void_p(B.data_ptr()), rank, in_flat, out_dim, float(scale), _stream())
+
+    def load_lora(self, path: str, strength: float = 1.0) -> dict:
+        """Apply every UNet module of a kohya-named LoRA safetensors file with
+        scale = strength * alpha / rank; returns the loader's counts."""
+        v = (c_int * 4)()
+        _call("dlm_unet_load_lora", self._h, path.encode(), float(strength), v, _stream())
+        return dict(zip(LORA_COUNT_FIELDS, list(v)))
+
+    def clear_loras(self):
+        """Restore every weight patched by apply_lora / load_lora bit-exactly."""
+        _call("dlm_unet_clear_loras", self._h, _stream())
+
+    def read_weight(self, name: str) -> torch.Tensor:
+        """The resident fp16 weight `name` as a CPU tensor in diffusers layout."""
+        shape = self._specs[name]
+        out = torch.empty(shape, dtype=torch.float16)
+        _call("dlm_unet_read_weight", self._h, name.encode(), c_void_p(out.data_ptr()),
+              out.numel() * 2, _stream())
         return out
 
     KERNEL_CLASSES = ("conv", "linear", "attention", "groupnorm", "layernorm", "other")

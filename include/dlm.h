@@ -195,6 +195,13 @@ int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias
 int dlm_conv_weight_pack_fp16(const void* w, void* out, int Cout, int Cin, int KH, int KW,
                               int Cin_pad, int ld_out, int col0, void* stream);
 
+/* Same layout as dlm_conv_weight_pack_fp16, accumulating instead of
+ * overwriting: out[...] = fp16(out[...] + w[...]) for ci < Cin; the padding
+ * channels are left unchanged.  Used to merge a LoRA delta into a packed
+ * conv weight (no counterpart in the reference, whose weights stay NCHW). */
+int dlm_conv_weight_pack_add_fp16(const void* w, void* out, int Cout, int Cin, int KH, int KW,
+                                  int Cin_pad, int ld_out, int col0, void* stream);
+
 /* Layout transposes: NCHW <-> NHWC (C_pad >= C channels in the NHWC side,
  * extra channels zero filled on the way in). */
 int dlm_nchw_to_nhwc_fp16(const void* in, void* out, int N, int C, int HW, int C_pad,

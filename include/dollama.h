@@ -64,6 +64,41 @@ int dlm_unet_forward(void* handle, int B, int H, int W, const void* latent,
                      const float* timesteps, const void* ehs, int ctx_len, const void* text,
                      const void* time_ids, int ids_bstride, void* out, void* stream);
 
+/* Runtime LoRA (reference src/infer/unet.cuh:97-114, unet.cu:373-458):
+ * W += scale * (B @ A) on the resident weight named base_key (diffusers
+ * name), A device fp16 [rank, in_flat], B device fp16 [out_dim, rank]
+ * (out_dim * in_flat = the weight's element count; 4-D conv weights are
+ * flattened as [Cout, Cin*KH*KW]).  The delta is rounded to fp16 before the
+ * add, as in the reference.  Synchronises the stream. */
+int dlm_unet_apply_lora(void* handle, const char* base_key, const void* A, const void* B, int rank,
+                        int in_flat, int out_dim, float scale, void* stream);
+/* Load a kohya-named LoRA safetensors file (lora_unet_<flat>.lora_down /
+ * .lora_up / .alpha; reference src/infer/lora.hpp:265-445) and apply every
+ * UNet module with scale = strength * alpha / rank.  counts (may be NULL)
+ * receives modules applied, text-encoder modules skipped, keys not
+ * understood, modules missing a half.  A module that matches no UNet weight
+ * is an error (DLM_ERR_STATE) and nothing after it is applied. */
+int dlm_unet_load_lora(void* handle, const char* path, float strength, int* counts /* [4] */,
+                       void* stream);
+/* Restore every weight patched since the last clear, bit-exactly. */
+int dlm_unet_clear_loras(void* handle, void* stream);
+/* Host only: resolve a LoRA file against the weight list of cfg without
+ * touching a device (reference load_lora_modules, src/infer/lora.hpp:265-445;
+ * same counts as dlm_unet_load_lora); fails like it on an unresolvable
+ * module.  fn (may be NULL) is called once per module that would be applied. */
+typedef void (*dlm_lora_module_fn)(const char* base_key, int rank, int in_flat, int out_dim,
+                                   float scale, void* user);
+int dlm_lora_scan(const dlm_unet_config* cfg, const char* path, float strength,
+                  int* counts /* [4] */, dlm_lora_module_fn fn, void* user);
+/* Copy a resident weight back to host memory as fp16 in its diffusers
+ * layout (reference unet_weight_device_ptr, src/infer/unet.cuh:114, the
+ * accessor its LoRA tests read weights through); bytes = 2 * numel. */
+int dlm_unet_read_weight(void* handle, const char* name, void* host_out, size_t bytes,
+                         void* stream);
+/* Host only: fp32 -> fp16 bits with round-to-nearest-even (the conversion
+ * the LoRA loader applies to F32 tensors). */
+int dlm_f32_to_f16(const float* in, uint16_t* out, size_t n);
+
 /* Stage hook for tests (src/infer/unet.cuh:53-54): called after the stream
  * is synchronised with (name, device pointer, element count, channel count);
  * activations are channels-last [B, H, W, C] except noise_pred (NCHW). */
