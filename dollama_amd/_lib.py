@@ -119,6 +119,7 @@ HIP_SIGNATURES = {
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),
     "dlm_gemm_force_tile": (I, [I]),
+    "dlm_gemm_force_split": (I, [I]),
 }
 
 

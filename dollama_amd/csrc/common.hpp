@@ -33,6 +33,14 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// MFMA 16x16x32 f16 -> f32 (gfx950):
+//   A (16 rows x 32 k): lane l holds row (l & 15), k = 8*(l >> 4) + [0..7]
+//   B (32 k x 16 cols): lane l holds col (l & 15), k = 8*(l >> 4) + [0..7]
+//   C/D (16 x 16):      lane l holds col (l & 15), rows 4*(l >> 4) + [0..3]
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ int mfma_row(int e, int lane) {
   return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
 }

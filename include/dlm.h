@@ -140,11 +140,19 @@ int dlm_conv_bias_residual_fp16(const void* conv, const void* convbias, const vo
 int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_period,
                                 void* stream);
 
-/* Tuning aid: force the MFMA GEMM / conv tile shape for every following
- * launch in this process (0 = automatic; 1 = 128x128, 2 = 128x64,
- * 3 = 64x64, 4 = 128x32, 5 = 256x128, 6 = 128x256, 7 = 256x256 output
- * tiles). */
+/* Tuning aids: force the MFMA GEMM / conv tile configuration, and the
+ * split-K factor, for every following launch in this process (0 =
+ * automatic).  Tiles 1-7: the register-staged core (128x128, 128x64, 64x64,
+ * 128x32, 256x128, 128x256, 256x256); 8-25: the LDS-DMA core
+ * (BMxBN, wave tile, ring depth) = 8 128x128 64x64 2, 9 128x64 64x32 2,
+ * 10 128x128 64x64 4, 11 128x64 64x32 4, 12 64x128 32x64 2,
+ * 13 256x128 128x64 2, 14 128x128 64x32 4, 15 128x128 64x32 2,
+ * 16 256x128 64x64 2, 17 128x128 32x64 4, 18 128x128 64x32 5,
+ * 19 256x128 64x64 3, 20 128x64 64x32 6, 21 256x160 64x80 3,
+ * 22 128x160 32x80 3, 23 128x160 64x80 2, 24 128x160 32x80 4,
+ * 25 64x160 32x80 2.  Splits apply to the LDS-DMA core only. */
 int dlm_gemm_force_tile(int tile_id);
+int dlm_gemm_force_split(int splits);
 
 /* ------------------------------------------------------------------ */
 /* Channels-last fused entry points (native forms used by the UNet)     */
