@@ -120,6 +120,7 @@ HIP_SIGNATURES = {
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),
     "dlm_gemm_force_tile": (I, [I]),
     "dlm_gemm_force_split": (I, [I]),
+    "dlm_gemm_set_variant": (I, [I]),
 }
 
 

@@ -1045,6 +1045,7 @@ static const SplitWorkspace* split_workspace(hipStream_t s) {
 }
 
 static int g_forced_split = 0;
+static int g_variant = 0;  // tuning aid: bits select alternative heuristics
 
 template <int BM, int BN, int WM, int WN, int NS, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
@@ -1155,21 +1156,25 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
                    : launch_dma<128, 128, 32, 64, 4>(ad, bd, ep, M, N, s);
       // Output widths that are multiples of 160 (SDXL's 320 / 640 / 1280
       // channels): 160-column tiles give whole waves of tiles on 256 CUs
-      // where 128-column tiles leave a partial wave.  Long K with few tiles
-      // is split so each CU still gets >= 22 slices.
+      // where 128-column tiles leave a partial wave; few tiles with a long K
+      // are split-K so every CU gets work.  Choices measured per UNet level
+      // (B=2): 32768x320 convs 256x160 (4 splits from 80 slices on), 8192 rows
+      // 128x160 up to 100 slices and 256x160 x2 splits beyond, 2048 rows
+      // 128x160 x2 splits from 44 slices, 256x160 x4 from 300.  Two splits of
+      // a grid that already fills the chip measured slower than one or four.
       const int nk = (int)ceil_div(bd.K, BK);
-      if (!ep.vt && N % 160 == 0) {
+      if (!ep.vt && N % 160 == 0 && !(g_variant & 1)) {
         const long long t256 = ceil_div(M, 256) * (N / 160), t160 = ceil_div(M, 128) * (N / 160);
-        const int ksplit = std::max(1, std::min(4, nk / 22));
-        if (t256 >= kCUs) return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, ksplit);
-        if (t160 >= 3 * kCUs / 4) {
-          if (nk >= 120 && t256 * 2 >= kCUs)
-            return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, 2);
-          return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
+        if (t256 >= kCUs)
+          return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, nk >= 80 ? 4 : 1);
+        if (t160 >= kCUs) {
+          if (nk <= 100) return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
+          return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, 2);
+        } else if (nk >= 300 && t256 * 4 >= kCUs) {
+          return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, 4);
+        } else if (nk >= 44 && t160 * 4 >= kCUs) {
+          return launch_dma<128, 160, 32, 80, 3>(ad, bd, ep, M, N, s, t160 * 2 >= kCUs ? 2 : 4);
         }
-        if (nk >= 44 && t160 * 2 >= kCUs / 2)
-          return launch_dma<128, 160, 32, 80, 3>(ad, bd, ep, M, N, s,
-                                                 (int)std::min<long long>(4, std::max<long long>(2, kCUs / t160)));
       }
       if (t128 >= kCUs / 2) {
         if (N % 128 != 0)
@@ -1687,6 +1692,12 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
 }
 
 }  // extern "C"
+
+extern "C" int dlm_gemm_set_variant(int variant) {
+  DLM_REQUIRE(variant >= 0, "variant must be >= 0");
+  dlm::g_variant = variant;
+  return DLM_OK;
+}
 
 extern "C" int dlm_gemm_force_split(int splits) {
   DLM_REQUIRE(splits >= 0 && splits <= 64, "splits must be in [0, 64]");

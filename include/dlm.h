@@ -153,6 +153,9 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
  * 25 64x160 32x80 2.  Splits apply to the LDS-DMA core only. */
 int dlm_gemm_force_tile(int tile_id);
 int dlm_gemm_force_split(int splits);
+/* Tuning aid: select alternative tile heuristics (0 = default; bit 0 = no
+ * 160-column / split-K rules). */
+int dlm_gemm_set_variant(int variant);
 
 /* ------------------------------------------------------------------ */
 /* Channels-last fused entry points (native forms used by the UNet)     */
