@@ -19,6 +19,8 @@
 //     is also lane-per-query and the online-softmax rescale is per lane.
 // Q, K, V and O are addressed with independent batch / token / head strides,
 // so the fused QKV projection output [B, S, 3C] is read in place.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace dlm {
@@ -211,8 +213,7 @@ __global__ void __launch_bounds__(256) flash_attn_d64_kernel(AttnParams p) {
 //     every 16 swapped), chosen so that the eight exponentiated scores a lane
 //     feeds to one P^T fragment belong to eight consecutive keys: the matching
 //     V^T fragment is then 16 contiguous bytes of a V^T row;
-//   * each wave owns QB blocks of 32 queries, sharing every K and V^T
-//     fragment read between them;
+//   * each wave owns one block of 32 queries;
 //   * the running max is kept on raw scores, p = 2^(s*c - m*c) is one FMA and
 //     one v_exp_f32 (c = scale * log2 e); masking runs only on a partial last
 //     key tile.
@@ -270,28 +271,33 @@ constexpr int FA_STAGE = 2 * FA_TILE;
 constexpr int FA_NS = 3;
 constexpr int kFaOOB = (int)0x80000000;
 
-template <int QB>
-__global__ void __launch_bounds__(256) flash_vt_kernel(FlashVtParams p) {
+// Software pipeline, one 32-query block per wave (more waves beat sharing
+// K/V fragments between two blocks: the softmax is VALU work that other
+// waves' MFMAs hide): the scores of tile kt+1 (MFMA) are issued before the
+// softmax of tile kt (VALU), so each wave's own MFMAs run in the shadow of
+// its exp / max / convert work.  The barrier that publishes tile kt+1 also
+// proves every wave is done with tile kt-1, whose buffer then receives tile
+// kt+2: one tile of DMA latency hidden, three buffers.  Full tiles carry no
+// masking code; the rescale is a real (rare) branch; the row sum is taken
+// over the fp16 P the MFMA consumes, two terms per dot2.
+__global__ void __launch_bounds__(256) flash_vt_pipe_kernel(FlashVtParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem_g[FA_NS * FA_STAGE];
   unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_g;
   const int b = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;
-  const int q0 = blockIdx.x * (128 * QB) + wave * (32 * QB);
+  const int q0 = blockIdx.x * 128 + wave * 32;
 
-  f16x8 qf[QB][4];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qi = q0 + qb * 32 + (lane & 31);
+  f16x8 qf[4];
+  {
+    const int qi = q0 + (lane & 31);
     const f16* qp = p.q + b * p.q_sb + h * p.q_sh + (long long)qi * p.q_ss + g * 8;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
-      qf[qb][ds] = qi < p.Sq ? *reinterpret_cast<const f16x8*>(qp + ds * 16) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      qf[ds] = qi < p.Sq ? *reinterpret_cast<const f16x8*>(qp + ds * 16) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
-  // DMA map: each tile is 64 rows x 8 chunks; wave w copies rows
-  // (w*2 + i)*8 + lane/8, i = 0, 1, of both the K and the V^T tile.
   const i32x4 rk = fa_rsrc(p.k, p.k_bytes);
   const i32x4 rv = fa_rsrc(p.vt, p.vt_bytes);
   int koff[2], kkey[2], voff[2], vkey[2];
@@ -322,129 +328,149 @@ __global__ void __launch_bounds__(256) flash_vt_kernel(FlashVtParams p) {
     const int c = chunk ^ ((row >> 1) & 7);
     return *reinterpret_cast<const f16x8 DLM_LDS*>(st + row * 128 + c * 16);
   };
+  // S^T = K Q^T of the tile in st: lane = query, element e of block kb = LDS
+  // key row kb*32 + 8*(e>>2) + 4g + (e&3)
+  auto scores = [&](const unsigned char DLM_LDS* st, f32x16 (&sv)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f16x8 kf[4];
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) kf[ds] = frag(st, kb * 32 + (lane & 31), 2 * ds + g);
+      sv[kb] = mfma32x32x16(kf[0], qf[0], f32x16{});
+#pragma unroll
+      for (int ds = 1; ds < 4; ++ds) sv[kb] = mfma32x32x16(kf[ds], qf[ds], sv[kb]);
+    }
+  };
 
   const int nkt = (p.Sk + FA_TK - 1) / FA_TK;
   issue(0, 0);
-  issue(1, min(1, nkt - 1));
+  if (nkt > 1) issue(1, 1);
 
-  float m_run[QB], l_run[QB];
-  f32x16 o[2][QB];
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x16 o[2];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m_run[qb] = -INFINITY;
-    l_run[qb] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      o[0][qb][e] = 0.0f;
-      o[1][qb][e] = 0.0f;
-    }
+  for (int e = 0; e < 16; ++e) {
+    o[0][e] = 0.0f;
+    o[1][e] = 0.0f;
   }
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    FA_WAIT_VM(4);  // the tile issued two iterations ago (four DMA per wave per tile)
+  // softmax of one tile's scores into fp16 P (see the lazy-rescale note above)
+  auto softmax = [&](f32x16 (&sv)[2], f16x8 (&pf)[4]) {
+    float mt = sv[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sv[kb][e]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const bool grow = (mt - m_run) * p.c > 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      asm volatile("" ::: "memory");  // a real branch: never evaluated speculatively
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * p.c);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        o[0][e] *= alpha;
+        o[1][e] *= alpha;
+      }
+    }
+    const float mc = m_run * p.c;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][e], p.c, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][e + 1], p.c, -mc));
+        const f16x2 hr = f16x2{(f16)p0, (f16)p1};
+        pf[kb * 2 + (e >> 3)][e & 7] = hr[0];
+        pf[kb * 2 + (e >> 3)][(e & 7) + 1] = hr[1];
+        lsum = __builtin_amdgcn_fdot2(hr, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+      }
+    l_run += lsum;
+  };
+  // O^T += V^T P^T over four 16-key steps (step j: tile keys 16j + 8g + [0, 8))
+  auto pv = [&](const f16x8 (&vf)[8], const f16x8 (&pf)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) o[dt] = mfma32x32x16(vf[j * 2 + dt], pf[j], o[dt]);
+  };
+  auto vread = [&](const unsigned char DLM_LDS* st, f16x8 (&vf)[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) vf[j * 2 + dt] = frag(st + FA_TILE, dt * 32 + (lane & 31), 2 * j + g);
+  };
+
+  // prologue: tile 0 published, its scores issued
+  if (nkt > 1) {
+    FA_WAIT_VM(4);
+  } else {
+    FA_WAIT_VM(0);
+  }
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  f32x16 sc[2];
+  scores(smem, sc);
+
+  int cur = 0;
+  for (int kt = 0; kt + 1 < nkt; ++kt) {
+    const int nxt = cur == FA_NS - 1 ? 0 : cur + 1;
+    const int nn = nxt == FA_NS - 1 ? 0 : nxt + 1;
+    FA_WAIT_VM(0);  // tile kt+1 (this wave's part)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    const unsigned char DLM_LDS* st = smem + (kt % FA_NS) * FA_STAGE;
-    issue((kt + 2) % FA_NS, min(kt + 2, nkt - 1));
-
-    // S^T = K Q^T: s[kb][qb], lane = query, element e = LDS key row
-    // kb*32 + 8*(e>>2) + 4g + (e&3)
-    f32x16 s[2][QB];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[kb][qb][e] = 0.0f;
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const f16x8 kf = frag(st, kb * 32 + (lane & 31), 2 * ds + g);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[kb][qb] = mfma32x32x16(kf, qf[qb][ds], s[kb][qb]);
-      }
-    }
-    if (kt * FA_TK + FA_TK > p.Sk) {  // partial last tile: keys past Sk do not exist
+    if (kt + 2 < nkt) issue(nn, kt + 2);
+    const unsigned char DLM_LDS* st = smem + cur * FA_STAGE;
+    f32x16 sn[2];
+    scores(smem + nxt * FA_STAGE, sn);  // tile kt+1, in the shadow of the softmax below
+    f16x8 vf[8];
+    vread(st, vf);
+    f16x8 pf[4];
+    softmax(sc, pf);  // tiles before the last are full: no mask
+    pv(vf, pf);
+    sc[0] = sn[0];
+    sc[1] = sn[1];
+    cur = nxt;
+  }
+  // last tile: its keys may end inside the tile
+  {
+    const int kt = nkt - 1;
+    if (kt * FA_TK + FA_TK > p.Sk) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int key = kt * FA_TK + fa_perm(kb * 32 + mfma_row(e, lane));
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            if (key >= p.Sk) s[kb][qb][e] = -INFINITY;
+          if (key >= p.Sk) sc[kb][e] = -INFINITY;
         }
     }
-
-    // Lazy rescale: the reference max m_run only moves when some lane's tile
-    // max exceeds it by more than 2^8 in the exp2 domain (a wave-uniform and,
-    // after the first tiles, rare branch); otherwise p = 2^((s - m_run) c)
-    // stays <= 256, exact in fp16 and harmless in the fp32 sums.
-    f16x8 pf[4][QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      float mt = s[0][qb][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][qb][e]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const bool grow = (mt - m_run[qb]) * p.c > 8.0f;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = fmaxf(m_run[qb], mt);
-        const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_new) * p.c);
-        m_run[qb] = m_new;
-        l_run[qb] *= alpha;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          o[0][qb][e] *= alpha;
-          o[1][qb][e] *= alpha;
-        }
-      }
-      const float mc = m_run[qb] * p.c;
-      float lsum = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][e], p.c, -mc));
-          lsum += pe;
-          pf[kb * 2 + (e >> 3)][qb][e & 7] = (f16)pe;
-        }
-      l_run[qb] += lsum;
-    }
-
-    // O^T += V^T P^T over four 16-key steps; step j covers tile keys
-    // 16j + 8g + [0, 8) for lane group g
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const f16x8 vf = frag(st + FA_TILE, dt * 32 + (lane & 31), 2 * j + g);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) o[dt][qb] = mfma32x32x16(vf, pf[j][qb], o[dt][qb]);
-      }
-    __builtin_amdgcn_sched_barrier(0);
+    f16x8 vf[8];
+    vread(smem + cur * FA_STAGE, vf);
+    f16x8 pf[4];
+    softmax(sc, pf);
+    pv(vf, pf);
   }
   FA_WAIT_VM(0);
 
+  const int qi = q0 + (lane & 31);
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (qi < p.Sq) {
+    f16* obase = p.o + b * p.o_sb + h * p.o_sh + (long long)qi * p.o_ss;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int qi = q0 + qb * 32 + (lane & 31);
-    const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
-    const float inv = 1.0f / l_tot;
-    if (qi < p.Sq) {
-      f16* obase = p.o + b * p.o_sb + h * p.o_sh + (long long)qi * p.o_ss;
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+      for (int gq = 0; gq < 4; ++gq) {
+        f16x4 r;
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          f16x4 r;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) r[t] = (f16)(o[dt][qb][4 * gq + t] * inv);
-          *reinterpret_cast<f16x4*>(obase + dt * 32 + 8 * gq + 4 * g) = r;
-        }
-    }
+        for (int t = 0; t < 4; ++t) r[t] = (f16)(o[dt][4 * gq + t] * inv);
+        *reinterpret_cast<f16x4*>(obase + dt * 32 + 8 * gq + 4 * g) = r;
+      }
   }
 }
 
@@ -463,14 +489,12 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   p.c = a->scale * 1.4426950408889634f;
   p.k_bytes = (unsigned)a->k_bytes;
   p.vt_bytes = (unsigned)a->vt_bytes;
+  // One 32-query block per wave: the softmax is VALU work that only other
+  // waves' MFMAs can hide, so more waves beat sharing K/V fragments between
+  // two query blocks (2x4096^2 x10 heads: 144 us vs 170 us).
   const long long wg2 = (long long)((a->Sq + 255) / 256) * a->H * a->B;
-  if (wg2 >= 256) {
-    const dim3 grid((a->Sq + 255) / 256, a->H, a->B);
-    hipLaunchKernelGGL(flash_vt_kernel<2>, grid, dim3(256), 0, s, p);
-  } else {
-    const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
-    hipLaunchKernelGGL(flash_vt_kernel<1>, grid, dim3(256), 0, s, p);
-  }
+  const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
+  hipLaunchKernelGGL(flash_vt_pipe_kernel, grid, dim3(256), 0, s, p);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
