@@ -1118,7 +1118,7 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
     switch (ep.act == DLM_ACT_GEGLU &&
                     (g_forced_tile == 9 || g_forced_tile == 11 || g_forced_tile == 14 ||
                      g_forced_tile == 15 || g_forced_tile == 18 || g_forced_tile == 20 ||
-                     (g_forced_tile >= 21 && g_forced_tile <= 25))
+                     (g_forced_tile >= 21 && g_forced_tile <= 26))
                 ? 0
                 : g_forced_tile) {
       case 8: return launch_dma<128, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
@@ -1139,6 +1139,7 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
       case 23: return launch_dma<128, 160, 64, 80, 2>(ad, bd, ep, M, N, s);
       case 24: return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
       case 25: return launch_dma<64, 160, 32, 80, 2>(ad, bd, ep, M, N, s);
+      case 26: return launch_dma<128, 80, 16, 80, 5>(ad, bd, ep, M, N, s);
       default: break;
     }
     if (g_forced_tile == 0 || ep.act == DLM_ACT_GEGLU) {
@@ -1163,7 +1164,14 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
       // 128x160 x2 splits from 44 slices, 256x160 x4 from 300.  Two splits of
       // a grid that already fills the chip measured slower than one or four.
       const int nk = (int)ceil_div(bd.K, BK);
-      if (!ep.vt && N % 160 == 0 && !(g_variant & 1)) {
+      // 2048-row outputs 1280 wide (one 1024-token level at B=2): 128x80
+      // tiles, 8 waves of 16x80, five-slice ring -> exactly 256 tiles
+      // (14.0 / 39.9 us at K = 1280 / 5120 against 15.1 / 43.9 for 128x128)
+      if (std::is_same<Desc, RowDesc>::value && !ep.vt && N % 80 == 0 &&
+          ceil_div(M, 128) * (N / 80) >= kCUs * 3 / 4 &&
+          ceil_div(M, 128) * (N / 80) <= kCUs && !(g_variant & 1))
+        return launch_dma<128, 80, 16, 80, 5>(ad, bd, ep, M, N, s);
+      if (!ep.vt && N % 160 == 0 && N <= 1280 && !(g_variant & 1)) {
         const long long t256 = ceil_div(M, 256) * (N / 160), t160 = ceil_div(M, 128) * (N / 160);
         if (t256 >= kCUs)
           return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, nk >= 80 ? 4 : 1);
@@ -1706,7 +1714,7 @@ extern "C" int dlm_gemm_force_split(int splits) {
 }
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 25, "tile_id must be in [0, 25]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 26, "tile_id must be in [0, 26]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

@@ -150,7 +150,8 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
  * 16 256x128 64x64 2, 17 128x128 32x64 4, 18 128x128 64x32 5,
  * 19 256x128 64x64 3, 20 128x64 64x32 6, 21 256x160 64x80 3,
  * 22 128x160 32x80 3, 23 128x160 64x80 2, 24 128x160 32x80 4,
- * 25 64x160 32x80 2.  Splits apply to the LDS-DMA core only. */
+ * 25 64x160 32x80 2, 26 128x80 16x80 5.  Splits apply to the LDS-DMA core
+ * only. */
 int dlm_gemm_force_tile(int tile_id);
 int dlm_gemm_force_split(int splits);
 /* Tuning aid: select alternative tile heuristics (0 = default; bit 0 = no
