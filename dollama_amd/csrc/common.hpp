@@ -51,6 +51,26 @@ __device__ __forceinline__ float gelu_erf_f(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
 }
 
+// erf by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26:
+// erf(z) = 1 - (a1 t + ... + a5 t^5) exp(-z^2), t = 1 / (1 + p z), z >= 0,
+// |error| <= 1.5e-7 (far below the fp16 output step).  Branch-free: one
+// reciprocal, one exp2, six FMAs; erf(-z) = -erf(z).
+__device__ __forceinline__ float erf_as(float x) {
+  const float z = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
+  float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  poly = __builtin_fmaf(poly, t, 1.421413741f);
+  poly = __builtin_fmaf(poly, t, -0.284496736f);
+  poly = __builtin_fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
+  const float r = __builtin_fmaf(-poly, e, 1.0f);
+  return __builtin_copysignf(r, x);
+}
+__device__ __forceinline__ float gelu_erf_fast(float x) {
+  return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
+}
+
 // Wave-wide reductions (wave64) through the cross-lane permute network.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
