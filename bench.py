@@ -233,7 +233,7 @@ def main():
             "bound": "mfma",
             "kernel": {"conv": "dma_gemm_kernel<ConvDesc> (implicit-GEMM conv, LDS-DMA)",
                        "linear": "dma_gemm_kernel<RowDesc> (linears, LDS-DMA)",
-                       "attention": "flash_vt_kernel (self) + flash_attn_d64_kernel (cross)"}[dom],
+                       "attention": "flash_vt_pipe_kernel (self and cross attention)"}[dom],
             "achieved": round(achieved, 1),
             "peak": MFMA_FP16_PEAK / 1e12,
             "unit": "TFLOP/s",
