@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--loop-steps", type=int, default=20, help="Euler loop length (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-runs", type=int, default=3)
+    ap.add_argument("--workload", choices=("unet", "vae"), default="unet",
+                    help="unet: the UNet step (default); vae: the VAE decode of one 1024x1024 image")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB (5 times), to scale the "
                          "FETCH_SIZE / WRITE_SIZE counters of a PMC run")
@@ -123,6 +125,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the UNet step "
               "is not sharded across GPUs in this build.", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "vae":
+        vae_main(args)
+        return
     import torch
     from dollama_amd import unet as U
     from dollama_amd.flops import unet_step_flops
@@ -246,6 +251,68 @@ def main():
         "euler_loop": loop,
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+def vae_main(args):
+    """SDXL VAE decode of one 128x128 latent into a 1024x1024 image (the
+    reference's only VAE shape), random-init weights ~N(0, 1/fan_in)."""
+    import torch
+    from dollama_amd import vae as V
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = V.SDXL_VAE_CONFIG
+    net = V.VAE(cfg)
+    w = V.random_weights(cfg, args.seed, device=dev)
+    net.set_weights(w)
+    net.prepare()
+    del w
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    lat = torch.randn(1, 4, 128, 128, generator=g, device=dev).half()
+    img = torch.empty(1, 3, 1024, 1024, dtype=torch.float16, device=dev)
+    for _ in range(args.warmup):
+        net.decode(lat, out=img)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        net.decode(lat, out=img)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    if not torch.isfinite(img.float()).all():
+        raise RuntimeError("non-finite image")
+    net.set_profiling(True)
+    reports = []
+    for _ in range(max(1, args.profile_runs)):
+        net.decode(lat, out=img)
+        reports.append(net.profile_report())
+    net.set_profiling(False)
+    classes = {}
+    flops = 0.0
+    for c in V.VAE.KERNEL_CLASSES:
+        ms_c = sorted(r[c]["ms"] for r in reports)[len(reports) // 2]
+        r0 = reports[-1][c]
+        flops += r0["flops"]
+        classes[c] = {"launches": r0["launches"], "ms": round(ms_c, 4),
+                      "tflops": round(r0["flops"] / (ms_c * 1e-3) / 1e12, 1) if r0["flops"] and ms_c else None,
+                      "gbps": round(r0["bytes"] / (ms_c * 1e-3) / 1e9, 1) if r0["bytes"] and ms_c else None}
+    line = {
+        "metric": "SDXL VAE decode ms @1024^2 (latent 128x128)",
+        "value": round(ms, 3), "unit": "ms/image", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16 operands, fp32 accumulate; fp32 up blocks 2-3",
+        "data": "synthetic: random-init SDXL VAE decoder weights N(0,1/fan_in), latent N(0,1)",
+        "config": {"workload": "sdxl_vae_decode_1024px", "batch": 1, "latent": [4, 128, 128],
+                   "params": 49490199},
+        "decode_tflop": round(flops / 1e12, 4),
+        "decode_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "frac_mfma": round(flops / (ms * 1e-3) / MFMA_FP16_PEAK, 4),
+        "classes": classes,
+        "reference_rtx5080_ms": 1000.9,
     }
     print(json.dumps(line), flush=True)
 

@@ -40,6 +40,7 @@ class ConvNhwcArgs(ctypes.Structure):
         ("bias", P), ("tbias", P), ("tbias_ld", I),
         ("residual", P), ("res_ld", I),
         ("out", P), ("ldy", I), ("out_nchw", I), ("act", I),
+        ("out_f32", I), ("res_f32", I),
     ]
 
 
@@ -118,6 +119,13 @@ HIP_SIGNATURES = {
     "dlm_linear_small_fp16": (I, [P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),
+    "dlm_linear_f32out_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, F, F, I, P]),
+    "dlm_group_norm_nhwc_f32in": (I, [P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
+    "dlm_cast_f32_to_f16": (I, [P, P, LL, F, P]),
+    "dlm_scale_fp16": (I, [P, LL, F, P]),
+    "dlm_latent_to_vae_fp16": (I, [P, P, LL, F, P]),
+    "dlm_image_to_rgb8": (I, [P, P, I, I, I, P]),
+    "dlm_softmax_rows_f32_fp16": (I, [P, LL, P, LL, I, I, P]),
     "dlm_gemm_force_tile": (I, [I]),
     "dlm_gemm_force_split": (I, [I]),
     "dlm_gemm_set_variant": (I, [I]),

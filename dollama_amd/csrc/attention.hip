@@ -520,6 +520,96 @@ int attention_strided(const dlm_attention_args* a, hipStream_t s) {
 
 static bool stride_ok(long long x) { return x % 8 == 0; }
 
+// ---------------------------------------------------------------------------
+// Row softmax of fp32 scores into fp16 probabilities: the middle step of the
+// VAE mid-block attention (one head, Dh = 512, S = h*w of the latent), which
+// runs as scores GEMM -> softmax -> P V GEMM instead of a flash kernel (the
+// reference's generic attention kernel, src/kernels/attention.cu:137-219,
+// likewise keeps a whole score row and takes a two-pass softmax).
+// One 256-thread block per row.  Rows up to 256 * 4 * VPT columns are held in
+// registers (one read of S); longer rows take a second read.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void block_max_sum(float& m, float& l, float* red) {
+  // merge (max, sum-of-exp) pairs: wave level, then across the 4 waves
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float mo = __shfl_xor(m, o, 64), lo = __shfl_xor(l, o, 64);
+    const float mn = fmaxf(m, mo);
+    l = (mn == -INFINITY) ? 0.0f : l * __expf(m - mn) + lo * __expf(mo - mn);
+    m = mn;
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * w] = m;
+    red[2 * w + 1] = l;
+  }
+  __syncthreads();
+  m = -INFINITY;
+  l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float mo = red[2 * i], lo = red[2 * i + 1];
+    const float mn = fmaxf(m, mo);
+    l = (mn == -INFINITY) ? 0.0f : l * __expf(m - mn) + lo * __expf(mo - mn);
+    m = mn;
+  }
+}
+
+template <int VPT>
+__global__ void __launch_bounds__(256)
+softmax_rows_kernel(const float* __restrict__ S, long long lds, f16* __restrict__ P, long long ldp,
+                    int cols) {
+  __shared__ float red[8];
+  const float* row = S + (size_t)blockIdx.x * lds;
+  f16* prow = P + (size_t)blockIdx.x * ldp;
+  const int nv = cols >> 2;
+  const int t = threadIdx.x;
+  float m = -INFINITY, l = 0.0f;
+  if (VPT > 0) {
+    float4 x[VPT > 0 ? VPT : 1];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = t + i * 256;
+      x[i] = v < nv ? reinterpret_cast<const float4*>(row)[v]
+                    : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      m = fmaxf(m, fmaxf(fmaxf(x[i].x, x[i].y), fmaxf(x[i].z, x[i].w)));
+    }
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        l += __expf(x[i].x - m) + __expf(x[i].y - m) + __expf(x[i].z - m) + __expf(x[i].w - m);
+    }
+    block_max_sum(m, l, red);
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = t + i * 256;
+      if (v < nv) {
+        const f16x4 o = {(f16)(__expf(x[i].x - m) * inv), (f16)(__expf(x[i].y - m) * inv),
+                         (f16)(__expf(x[i].z - m) * inv), (f16)(__expf(x[i].w - m) * inv)};
+        *reinterpret_cast<f16x4*>(prow + 4 * v) = o;
+      }
+    }
+  } else {
+    for (int v = t; v < nv; v += 256) {
+      const float4 x = reinterpret_cast<const float4*>(row)[v];
+      const float mx = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
+      const float mn = fmaxf(m, mx);
+      l = l * __expf(m - mn) + __expf(x.x - mn) + __expf(x.y - mn) + __expf(x.z - mn) +
+          __expf(x.w - mn);
+      m = mn;
+    }
+    block_max_sum(m, l, red);
+    const float inv = 1.0f / l;
+    for (int v = t; v < nv; v += 256) {
+      const float4 x = reinterpret_cast<const float4*>(row)[v];
+      const f16x4 o = {(f16)(__expf(x.x - m) * inv), (f16)(__expf(x.y - m) * inv),
+                       (f16)(__expf(x.z - m) * inv), (f16)(__expf(x.w - m) * inv)};
+      *reinterpret_cast<f16x4*>(prow + 4 * v) = o;
+    }
+  }
+}
+
 }  // namespace dlm
 
 using namespace dlm;
@@ -566,6 +656,26 @@ int dlm_attention_vt_fp16(const dlm_attention_vt_args* a, void* stream) {
   DLM_REQUIRE(klast <= (long long)a->k_bytes && vlast <= (long long)a->vt_bytes,
               "K or V^T extends past its buffer size");
   return attention_vt(a, (hipStream_t)stream);
+}
+
+int dlm_softmax_rows_f32_fp16(const float* S, long long lds, void* P, long long ldp, int rows,
+                              int cols, void* stream) {
+  if (rows <= 0 || cols <= 0) return DLM_OK;
+  DLM_REQUIRE(S && P, "NULL pointer");
+  DLM_REQUIRE(cols % 4 == 0 && lds % 4 == 0 && ldp % 4 == 0 && lds >= cols && ldp >= cols,
+              "cols, lds and ldp must be multiples of 4 with lds, ldp >= cols");
+  DLM_REQUIRE(dlm_aligned16(S) && ((uintptr_t)P & 7) == 0, "S must be 16-byte, P 8-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (cols <= 256 * 4 * 4)
+    hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(rows), dim3(256), 0, s, S, lds, (f16*)P, ldp, cols);
+  else if (cols <= 256 * 4 * 16)
+    hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(rows), dim3(256), 0, s, S, lds, (f16*)P, ldp,
+                       cols);
+  else
+    hipLaunchKernelGGL(softmax_rows_kernel<0>, dim3(rows), dim3(256), 0, s, S, lds, (f16*)P, ldp,
+                       cols);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
 }
 
 int dlm_attention_fp16(const void* q, const void* k, const void* v, void* out, int B, int H,

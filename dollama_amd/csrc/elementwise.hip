@@ -179,6 +179,47 @@ __global__ void scale_latent_kernel(const float* latent, f16* model_in, int n, f
   }
 }
 
+// out = fp16(in * scale); eight elements per vector step, scalar tail.
+__global__ void cast_f32_f16_kernel(const float* __restrict__ in, f16* __restrict__ out,
+                                    long long n, float scale) {
+  const long long n8 = n >> 3;
+  GRID_STRIDE(i, n8) {
+    const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
+    const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
+    const f16x8 o = {(f16)(a.x * scale), (f16)(a.y * scale), (f16)(a.z * scale), (f16)(a.w * scale),
+                     (f16)(b.x * scale), (f16)(b.y * scale), (f16)(b.z * scale), (f16)(b.w * scale)};
+    reinterpret_cast<f16x8*>(out)[i] = o;
+  }
+  GRID_STRIDE(j, n - (n8 << 3)) out[(n8 << 3) + j] = (f16)(in[(n8 << 3) + j] * scale);
+}
+
+__global__ void scale_f16_kernel(f16* x, long long n, float scale) {
+  GRID_STRIDE(i, n) x[i] = (f16)((float)x[i] * scale);
+}
+
+// VAE input: fp16(latent / scaling_factor) (reference src/infer/diffusion.cu:980-984).
+__global__ void latent_to_vae_kernel(const float* latent, f16* out, long long n, float sf) {
+  GRID_STRIDE(i, n) out[i] = (f16)(latent[i] / sf);
+}
+
+// Decoded image [N, 3, H, W] fp16 in [-1, 1] -> RGB8 [N, H, W, 3]:
+// q = int(clamp(v * 0.5 + 0.5, 0, 1) * 255 + 0.5) (reference image_f16_to_rgb_u8,
+// src/infer/diffusion.cu:146-165); a NaN maps to 0.
+__global__ void image_to_rgb8_kernel(const f16* img, uint8_t* rgb, long long HW, long long n) {
+  GRID_STRIDE(i, n) {  // i = (b * HW + p) * 3 + c
+    const long long c = i % 3, bp = i / 3;
+    const long long b = bp / HW, p = bp - b * HW;
+    const float v = (float)img[(b * 3 + c) * HW + p];
+    // separately rounded multiply and add, as the reference's host code
+    // computes them (no fused multiply-add)
+    float n01 = __fadd_rn(__fmul_rn(v, 0.5f), 0.5f);
+    n01 = n01 < 0.0f ? 0.0f : n01;
+    n01 = n01 > 1.0f ? 1.0f : n01;
+    const int q = n01 == n01 ? (int)__fadd_rn(__fmul_rn(n01, 255.0f), 0.5f) : 0;
+    rgb[i] = (uint8_t)(q < 0 ? 0 : (q > 255 ? 255 : q));
+  }
+}
+
 }  // namespace dlm
 
 using namespace dlm;
@@ -329,6 +370,46 @@ int dlm_euler_cfg_step(float* latent, const void* noise, void* model_in, int n, 
   hipLaunchKernelGGL(euler_cfg_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      latent, (const f16*)noise, (f16*)model_in, n, guidance, sigma_next - sigma,
                      in_scale);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_cast_f32_to_f16(const float* in, void* out, long long n, float scale, void* stream) {
+  if (n <= 0) return DLM_OK;
+  DLM_REQUIRE(in && out, "NULL pointer");
+  DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(out), "buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(grid_for(std::max(n >> 3, 1LL))), dim3(256), 0,
+                     (hipStream_t)stream, in, (f16*)out, n, scale);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_scale_fp16(void* x, long long n, float scale, void* stream) {
+  if (n <= 0) return DLM_OK;
+  DLM_REQUIRE(x, "NULL pointer");
+  hipLaunchKernelGGL(scale_f16_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+                     (f16*)x, n, scale);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_latent_to_vae_fp16(const float* latent, void* out, long long n, float scaling_factor,
+                           void* stream) {
+  if (n <= 0) return DLM_OK;
+  DLM_REQUIRE(latent && out, "NULL pointer");
+  DLM_REQUIRE(scaling_factor != 0.0f, "scaling_factor must be non-zero");
+  hipLaunchKernelGGL(latent_to_vae_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+                     latent, (f16*)out, n, scaling_factor);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_image_to_rgb8(const void* image, uint8_t* rgb, int N, int H, int W, void* stream) {
+  if (N <= 0 || H <= 0 || W <= 0) return DLM_OK;
+  DLM_REQUIRE(image && rgb, "NULL pointer");
+  const long long HW = (long long)H * W, n = (long long)N * HW * 3;
+  hipLaunchKernelGGL(image_to_rgb8_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+                     (const f16*)image, rgb, HW, n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

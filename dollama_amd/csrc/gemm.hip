@@ -55,6 +55,11 @@ struct EpiArgs {
   int vt_col0;
   int vt_tokens;
   int vt_ld;
+  // fp32 output (y holds floats) / fp32 residual (res holds floats): the
+  // wide-range paths (VAE decoder stages whose pre-residual sums leave the
+  // fp16 range, attention scores ahead of a softmax)
+  int y_f32;
+  int res_f32;
 };
 
 // ---------------------------------------------------------------------------
@@ -265,11 +270,16 @@ __device__ __forceinline__ void epilogue_tile(const f32x16& a, int row0, int col
       if (ep.tbias) v += (float)ep.tbias[(size_t)n * ep.tbias_ld + col];
       if (ep.act == DLM_ACT_SILU) v = silu_f(v);
       else if (ep.act == DLM_ACT_GELU) v = gelu_erf_f(v);
-      if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + col];
-      if (ep.out_nchw)
-        ep.y[((size_t)n * ep.N + col) * ep.rows_per_sample + p] = (f16)v;
+      if (ep.res) {
+        const size_t ri = (size_t)row * ep.ldr + col;
+        v += ep.beta * (ep.res_f32 ? reinterpret_cast<const float*>(ep.res)[ri] : (float)ep.res[ri]);
+      }
+      const size_t yi = ep.out_nchw ? ((size_t)n * ep.N + col) * ep.rows_per_sample + p
+                                    : (size_t)row * ep.ldy + col;
+      if (ep.y_f32)
+        reinterpret_cast<float*>(ep.y)[yi] = v;
       else
-        ep.y[(size_t)row * ep.ldy + col] = (f16)v;
+        ep.y[yi] = (f16)v;
     }
   }
 }
@@ -712,11 +722,28 @@ __device__ __forceinline__ void epi4(const f32x4& a, int row, int col, const Epi
     for (int t = 0; t < 4; ++t) v[t] = gelu_erf_f(v[t]);
   }
   if (ep.res) {
-    const f16x4 r = ld4h(ep.res + (size_t)row * ep.ldr + col);
+    if (ep.res_f32) {
+      const float4 r =
+          *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ep.res) + (size_t)row * ep.ldr + col);
+      v[0] += ep.beta * r.x;
+      v[1] += ep.beta * r.y;
+      v[2] += ep.beta * r.z;
+      v[3] += ep.beta * r.w;
+    } else {
+      const f16x4 r = ld4h(ep.res + (size_t)row * ep.ldr + col);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)r[t];
+      for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)r[t];
+    }
   }
-  if (ep.vt && col >= ep.vt_col0) {
+  if (ep.y_f32) {
+    float* y = reinterpret_cast<float*>(ep.y);
+    if (ep.out_nchw) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) y[((size_t)n * ep.N + col + t) * ep.rows_per_sample + p] = v[t];
+    } else {
+      *reinterpret_cast<float4*>(y + (size_t)row * ep.ldy + col) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  } else if (ep.vt && col >= ep.vt_col0) {
     const int smp = row / ep.vt_tokens;
     const int tok = row - smp * ep.vt_tokens;
     f16* dst = ep.vt + ((size_t)smp * (ep.N - ep.vt_col0) + (col - ep.vt_col0)) * ep.vt_ld + tok;
@@ -1099,7 +1126,9 @@ static bool al8(const void* p) { return ((uintptr_t)p & 7) == 0; }
 static bool dma_epilogue_ok(const EpiArgs& ep) {
   if (ep.N % 4 != 0 || !al8(ep.y) || (ep.bias && !al8(ep.bias))) return false;
   if (!ep.out_nchw && ep.ldy % 4 != 0) return false;
+  if (ep.y_f32 && !ep.out_nchw && !dlm_aligned16(ep.y)) return false;
   if (ep.res && (ep.ldr % 4 != 0 || !al8(ep.res))) return false;
+  if (ep.res && ep.res_f32 && !dlm_aligned16(ep.res)) return false;
   if (ep.tbias && (ep.tbias_ld % 4 != 0 || !al8(ep.tbias))) return false;
   return true;
 }
@@ -1112,6 +1141,8 @@ template <class Desc>
 static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                        hipStream_t s) {
   constexpr int kCUs = 256;
+  if ((ep.y_f32 || ep.res_f32) && (ep.vt || ep.act == DLM_ACT_GEGLU))
+    return fail(DLM_ERR_UNSUPPORTED, "fp32 output/residual with a GEGLU or V^T epilogue");
   const bool dma = dma_epilogue_ok(ep) && dma_operand_ok(ad) && dma_operand_ok(bd);
   if (dma) {
     // GEGLU pairs value/gate blocks inside one wave: only 64-column waves
@@ -1243,6 +1274,8 @@ static EpiArgs make_epi(void* Y, int ldy, const void* bias, const void* R, int l
   ep.vt_col0 = 0;
   ep.vt_tokens = 0;
   ep.vt_ld = 0;
+  ep.y_f32 = 0;
+  ep.res_f32 = 0;
   return ep;
 }
 
@@ -1444,6 +1477,8 @@ int conv_nhwc_impl(const dlm_conv_nhwc_args* a, hipStream_t s) {
   ep.tbias_ld = a->tbias_ld;
   ep.rows_per_sample = d.HoWo;
   ep.out_nchw = a->out_nchw;
+  ep.y_f32 = a->out_f32 ? 1 : 0;
+  ep.res_f32 = a->res_f32 ? 1 : 0;
   return launch_gemm(d, bd, ep, d.M, a->Cout, s);
 }
 
@@ -1503,6 +1538,27 @@ int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const voi
   ep.vt_col0 = vt_col0;
   ep.vt_tokens = tokens;
   ep.vt_ld = vt_ld;
+  return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
+}
+
+int dlm_linear_f32out_fp16(const void* X, int lda, const void* W, int ldw, const void* bias,
+                           const float* R, int ldr, float* Y, int ldy, int M, int N, int K,
+                           float alpha, float beta, int act, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(X && W && Y, "NULL operand");
+  DLM_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K, lda and ldw must be multiples of 8");
+  DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
+  DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
+  DLM_REQUIRE(2LL * M * lda < (1LL << 31) && 2LL * N * ldw < (1LL << 31),
+              "X or W larger than 2 GiB");
+  DLM_REQUIRE(act == DLM_ACT_NONE || act == DLM_ACT_SILU || act == DLM_ACT_GELU,
+              "act must be none/silu/gelu");
+  DLM_REQUIRE(ldy >= N && (!R || ldr >= N), "ldy/ldr smaller than N");
+  RowDesc ad{(const f16*)X, lda, M, K, (unsigned)((size_t)M * lda * 2)};
+  RowDesc bd{(const f16*)W, ldw, N, K, (unsigned)((size_t)N * ldw * 2)};
+  EpiArgs ep = make_epi(Y, ldy, bias, R, ldr, M, N, alpha, beta, act);
+  ep.y_f32 = 1;
+  ep.res_f32 = 1;
   return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
 }
 

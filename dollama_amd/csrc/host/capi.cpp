@@ -15,6 +15,7 @@
 #include "safetensors.hpp"
 #include "scheduler.hpp"
 #include "unet.hpp"
+#include "vae.hpp"
 
 using namespace dollama;
 
@@ -54,6 +55,28 @@ UNetConfig to_cfg(const dlm_unet_config* c) {
   u.out_channels = c->out_channels;
   u.groups = c->groups;
   return u;
+}
+
+VaeConfig to_vcfg(const dlm_vae_config* c) {
+  VaeConfig v;
+  for (int i = 0; i < 4; ++i) v.ch[i] = c->ch[i];
+  v.latent_channels = c->latent_channels;
+  v.out_channels = c->out_channels;
+  v.layers = c->layers;
+  v.groups = c->groups;
+  v.fp32_from = c->fp32_from;
+  return v;
+}
+
+void spec_out(const std::vector<WeightSpec>& specs, int index, char* name, int name_len, int* ndim,
+              int64_t* shape) {
+  if (!name || name_len <= 0 || !ndim || !shape) throw std::invalid_argument("NULL argument");
+  if (index < 0 || index >= (int)specs.size()) throw std::invalid_argument("index out of range");
+  const WeightSpec& s = specs[index];
+  if ((int)s.name.size() >= name_len) throw std::invalid_argument("name buffer too small");
+  std::memcpy(name, s.name.c_str(), s.name.size() + 1);
+  *ndim = (int)s.shape.size();
+  for (int i = 0; i < 4; ++i) shape[i] = i < *ndim ? s.shape[i] : 0;
 }
 
 DeviceArenaId arena_id(int id) {
@@ -299,6 +322,124 @@ int dlm_pipeline_denoise(void* unet, int steps, float guidance, int H, int W, fl
     a.text = text;
     a.time_ids = time_ids;
     denoise(*static_cast<UNet*>(unet), a, stream);
+  });
+}
+
+int dlm_vae_config_sdxl(dlm_vae_config* cfg) {
+  return guarded([&] {
+    if (!cfg) throw std::invalid_argument("NULL cfg");
+    const VaeConfig v;
+    for (int i = 0; i < 4; ++i) cfg->ch[i] = v.ch[i];
+    cfg->latent_channels = v.latent_channels;
+    cfg->out_channels = v.out_channels;
+    cfg->layers = v.layers;
+    cfg->groups = v.groups;
+    cfg->fp32_from = v.fp32_from;
+  });
+}
+
+int dlm_vae_weight_count(const dlm_vae_config* cfg, int* count) {
+  return guarded([&] {
+    if (!cfg || !count) throw std::invalid_argument("NULL argument");
+    *count = (int)vae_weight_specs(to_vcfg(cfg)).size();
+  });
+}
+
+int dlm_vae_weight_spec(const dlm_vae_config* cfg, int index, char* name, int name_len, int* ndim,
+                        int64_t* shape) {
+  return guarded([&] {
+    if (!cfg) throw std::invalid_argument("NULL cfg");
+    spec_out(vae_weight_specs(to_vcfg(cfg)), index, name, name_len, ndim, shape);
+  });
+}
+
+int dlm_vae_create(const dlm_vae_config* cfg, void** handle) {
+  return guarded([&] {
+    if (!cfg || !handle) throw std::invalid_argument("NULL argument");
+    *handle = nullptr;
+    *handle = new VAE(to_vcfg(cfg));
+  });
+}
+
+int dlm_vae_destroy(void* handle) {
+  return guarded([&] { delete static_cast<VAE*>(handle); });
+}
+
+int dlm_vae_set_weight(void* handle, const char* name, const void* dptr, int ndim,
+                       const int64_t* shape) {
+  return guarded([&] {
+    if (!handle || !name || ndim < 0 || ndim > 8 || (ndim > 0 && !shape))
+      throw std::invalid_argument("bad argument");
+    std::vector<int64_t> s(shape, shape + ndim);
+    static_cast<VAE*>(handle)->set_weight(name, dptr, s);
+  });
+}
+
+int dlm_vae_prepare(void* handle, void* stream) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<VAE*>(handle)->prepare(stream);
+  });
+}
+
+int dlm_vae_load_safetensors(void* handle, const char* path, void* stream) {
+  return guarded([&] {
+    if (!handle || !path) throw std::invalid_argument("NULL argument");
+    VAE* v = static_cast<VAE*>(handle);
+    SafeTensors st(path);
+    void* dev = nullptr;
+    DLM_CALL(dlm_malloc(&dev, st.data_bytes()));
+    std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
+    DLM_CALL(dlm_memcpy(dev, st.data(), st.data_bytes(), 0));
+    for (const WeightSpec& s : vae_weight_specs(v->config())) {
+      if (!st.has(s.name)) throw std::runtime_error("safetensors: missing '" + s.name + "'");
+      if (st.dtype(s.name) != StDtype::F16)
+        throw std::runtime_error("safetensors: '" + s.name + "' is not F16");
+      if (st.offset(s.name) % 2 != 0) throw std::runtime_error("safetensors: misaligned tensor");
+      v->set_weight(s.name, static_cast<char*>(dev) + st.offset(s.name), st.shape(s.name));
+    }
+    v->prepare(stream);
+  });
+}
+
+int dlm_vae_packed_bytes(void* handle, size_t* bytes) {
+  return guarded([&] {
+    if (!handle || !bytes) throw std::invalid_argument("NULL argument");
+    *bytes = static_cast<VAE*>(handle)->packed_bytes();
+  });
+}
+
+int dlm_vae_decode(void* handle, int N, int h, int w, const void* latent, void* image, void* stream) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<VAE*>(handle)->decode(N, h, w, latent, image, stream);
+  });
+}
+
+int dlm_vae_set_stage_hook(void* handle, dlm_vae_stage_hook hook, void* user) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<VAE*>(handle)->set_stage_hook(hook, user);
+  });
+}
+
+int dlm_vae_set_profiling(void* handle, int on) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<VAE*>(handle)->set_profiling(on != 0);
+  });
+}
+
+int dlm_vae_profile_report(void* handle, double* out, void* stream) {
+  return guarded([&] {
+    if (!handle || !out) throw std::invalid_argument("NULL argument");
+    const auto r = static_cast<VAE*>(handle)->profile_report(stream);
+    for (size_t c = 0; c < r.size() && c < 5; ++c) {
+      out[4 * c + 0] = r[c].count;
+      out[4 * c + 1] = r[c].ms;
+      out[4 * c + 2] = r[c].flops;
+      out[4 * c + 3] = r[c].bytes;
+    }
   });
 }
 

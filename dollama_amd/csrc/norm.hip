@@ -53,13 +53,22 @@ __device__ __forceinline__ void load8(const f16* p, float (&v)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = (float)x[i];
 }
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+  const float4 x0 = reinterpret_cast<const float4*>(p)[0];
+  const float4 x1 = reinterpret_cast<const float4*>(p)[1];
+  v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+  v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+}
 
 // partial[n][chunk][g] = (mean, M2) of group g over the chunk's pixels.
 // Per-channel sums are shifted by the chunk's first pixel, reduced over the R
 // rows in LDS, turned into per-channel (mean, M2) and combined per group with
 // the equal-count form of Chan's formula.
-__global__ void gn_partial_kernel(const f16* __restrict__ a, int Ca, int lda,
-                                  const f16* __restrict__ b, int ldb, int HW, int C, int G,
+// T is the activation type: fp16, or fp32 for the VAE decoder's wide-range
+// stages (reference k_group_norm_f32, src/kernels/vae_decode.cu:466-545).
+template <typename T>
+__global__ void gn_partial_kernel(const T* __restrict__ a, int Ca, int lda,
+                                  const T* __restrict__ b, int ldb, int HW, int C, int G,
                                   int chunk, int chunks, int S, int R,
                                   float2* __restrict__ partial) {
   extern __shared__ float2 red[];  // [R][C], reused as [C] per-channel (mean, M2)
@@ -67,7 +76,7 @@ __global__ void gn_partial_kernel(const f16* __restrict__ a, int Ca, int lda,
   const int tid = threadIdx.x;
   const int s = tid % S, r = tid / S;
   const int c = s * 8;
-  const f16* src;
+  const T* src;
   int ld;
   if (c < Ca) {
     src = a + (size_t)n * HW * lda + c;
@@ -181,8 +190,9 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
   }
 }
 
-__global__ void gn_apply_kernel(const f16* __restrict__ a, int Ca, int lda,
-                                const f16* __restrict__ b, int ldb, f16* __restrict__ out,
+template <typename T>
+__global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
+                                const T* __restrict__ b, int ldb, f16* __restrict__ out,
                                 int ldo, int HW, int C, int total_vec,
                                 const float2* __restrict__ ss, int silu) {
   const int S = C / 8;
@@ -191,7 +201,7 @@ __global__ void gn_apply_kernel(const f16* __restrict__ a, int Ca, int lda,
     const int s = v - row * S;
     const int n = row / HW;
     const int c = s * 8;
-    const f16* src = c < Ca ? a + (size_t)row * lda + c : b + (size_t)row * ldb + (c - Ca);
+    const T* src = c < Ca ? a + (size_t)row * lda + c : b + (size_t)row * ldb + (c - Ca);
     float x[8];
     load8(src, x);
     const float4* ssv = reinterpret_cast<const float4*>(ss + (size_t)n * C + c);
@@ -212,32 +222,42 @@ __global__ void gn_apply_kernel(const f16* __restrict__ a, int Ca, int lda,
   }
 }
 
-int group_norm_nhwc(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
-                    const void* gamma, const void* beta, void* out, int ld_out, int N, int HW,
-                    int C, int G, float eps, int silu, void* ws, hipStream_t s) {
+template <typename T>
+static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
+                             const void* gamma, const void* beta, void* out, int ld_out, int N,
+                             int HW, int C, int G, float eps, int silu, void* ws, hipStream_t s) {
   const GnPlan p = gn_plan(N, C, HW);
   float2* partial = (float2*)ws;
   float2* ss = partial + (size_t)N * p.chunks * G;
   ss = (float2*)(((uintptr_t)ss + 15) & ~(uintptr_t)15);
-  const f16* a = (const f16*)in_a;
-  const f16* b = in_b ? (const f16*)in_b : a;
+  const T* a = (const T*)in_a;
+  const T* b = in_b ? (const T*)in_b : a;
+  const long long total_vec = (long long)N * HW * (C / 8);
+  if (total_vec >= (1LL << 31) || (long long)N * HW * std::max(ld_a, ld_out) >= (1LL << 31))
+    return fail(DLM_ERR_UNSUPPORTED, "group_norm: tensor too large for 32-bit indexing");
   const size_t red_bytes = (size_t)p.R * C * sizeof(float2);
   if (red_bytes > 160 * 1024)
     return fail(DLM_ERR_UNSUPPORTED, "group_norm: channel count too large for one block");
-  hipLaunchKernelGGL(gn_partial_kernel, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
+  hipLaunchKernelGGL(gn_partial_kernel<T>, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
                      ld_a, b, ld_b, HW, C, G, p.chunk, p.chunks, p.S, p.R, partial);
   DLM_LAUNCH_CHECK();
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
                      p.chunks, (const f16*)gamma, (const f16*)beta, eps, ss);
   DLM_LAUNCH_CHECK();
-  const long long total_vec = (long long)N * HW * (C / 8);
-  if (total_vec >= (1LL << 31) || (long long)N * HW * std::max(ld_a, ld_out) >= (1LL << 31))
-    return fail(DLM_ERR_UNSUPPORTED, "group_norm: tensor too large for 32-bit indexing");
   const int blocks = (int)std::min<long long>((total_vec + 255) / 256, 8192);
-  hipLaunchKernelGGL(gn_apply_kernel, dim3(blocks), dim3(256), 0, s, a, C_a, ld_a, b, ld_b,
+  hipLaunchKernelGGL(gn_apply_kernel<T>, dim3(blocks), dim3(256), 0, s, a, C_a, ld_a, b, ld_b,
                      (f16*)out, ld_out, HW, C, (int)total_vec, ss, silu);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
+}
+
+int group_norm_nhwc(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
+                    const void* gamma, const void* beta, void* out, int ld_out, int N, int HW,
+                    int C, int G, float eps, int silu, void* ws, hipStream_t s, bool in_f32 = false) {
+  return in_f32 ? group_norm_nhwc_t<float>(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N,
+                                           HW, C, G, eps, silu, ws, s)
+                : group_norm_nhwc_t<f16>(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N,
+                                         HW, C, G, eps, silu, ws, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -376,6 +396,20 @@ int dlm_group_norm_nhwc_fp16(const void* in_a, int C_a, int ld_a, const void* in
   DLM_REQUIRE(dlm_aligned16(workspace), "workspace must be 16-byte aligned");
   return group_norm_nhwc(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N, HW, C,
                          num_groups, eps, fuse_silu, workspace, (hipStream_t)stream);
+}
+
+int dlm_group_norm_nhwc_f32in(const float* in, int ld_in, const void* gamma, const void* beta,
+                              void* out, int ld_out, int N, int HW, int C, int num_groups,
+                              float eps, int fuse_silu, void* workspace, void* stream) {
+  if (N <= 0 || HW <= 0 || C <= 0 || num_groups <= 0) return DLM_OK;
+  DLM_REQUIRE(in && out && workspace, "NULL pointer");
+  DLM_REQUIRE(C % num_groups == 0, "C must be divisible by num_groups");
+  DLM_REQUIRE(C % 8 == 0, "C must be a multiple of 8");
+  DLM_REQUIRE(ld_in % 8 == 0 && ld_in >= C && ld_out % 8 == 0 && ld_out >= C, "bad row strides");
+  DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(out) && dlm_aligned16(workspace),
+              "buffers must be 16-byte aligned");
+  return group_norm_nhwc(in, C, ld_in, nullptr, 0, gamma, beta, out, ld_out, N, HW, C, num_groups,
+                         eps, fuse_silu, workspace, (hipStream_t)stream, true);
 }
 
 int dlm_group_norm_fp16(const void* in, const void* gamma, const void* beta, void* out, int N,

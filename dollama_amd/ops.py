@@ -274,6 +274,45 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias=None, residual=None, act=ACT_N
     return out
 
 
+def linear_f32out(x: torch.Tensor, w: torch.Tensor, bias=None, residual=None, act=ACT_NONE,
+                  out=None, alpha=1.0, beta=1.0) -> torch.Tensor:
+    """fp32 y = act(alpha * x @ w.T + bias) + beta * residual (fp32 residual);
+    x [M,K], w [N,K] fp16."""
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError("w.shape[1] != K")
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    _need(x, M * K, "x")
+    _need(w, N * K, "w")
+    _need(bias, N, "bias", optional=True)
+    _need(residual, M * N, "residual", optional=True, dtype=torch.float32)
+    _need(out, M * N, "out", dtype=torch.float32)
+    call("dlm_linear_f32out_fp16", _p(x), K, _p(w), K, _p(bias), _p(residual), N, _p(out), N,
+         M, N, K, float(alpha), float(beta), int(act), stream_handle())
+    return out
+
+
+def softmax_rows(s: torch.Tensor, out=None) -> torch.Tensor:
+    """fp16 softmax over the last dim of fp32 [rows, cols]."""
+    rows, cols = s.shape
+    if out is None:
+        out = torch.empty(rows, cols, dtype=torch.float16, device=s.device)
+    _need(s, rows * cols, "s", dtype=torch.float32)
+    _need(out, rows * cols, "out")
+    call("dlm_softmax_rows_f32_fp16", _p(s), cols, _p(out), cols, rows, cols, stream_handle())
+    return out
+
+
+def cast_f32_to_f16(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """fp16(x * scale)."""
+    _need(x, x.numel(), "x", dtype=torch.float32)
+    out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    call("dlm_cast_f32_to_f16", _p(x), _p(out), x.numel(), float(scale), stream_handle())
+    return out
+
+
 def linear_vt(x: torch.Tensor, w: torch.Tensor, vt_col0: int, tokens: int, bias=None, vt_ld=None):
     """y = x @ w.T for columns [0, vt_col0) as [M, vt_col0], and the remaining
     columns transposed per sample as vt [M // tokens, N - vt_col0, vt_ld]
@@ -341,10 +380,11 @@ def conv2d_nhwc(x: torch.Tensor, w_packed: torch.Tensor, *, KH: int, KW: int, st
                 bias=None, tbias=None, residual=None, x_b: Optional[torch.Tensor] = None,
                 upsample=False, shortcut: Optional[torch.Tensor] = None,
                 shortcut_b: Optional[torch.Tensor] = None, act=ACT_NONE, out=None,
-                out_nchw=False, cout: Optional[int] = None) -> torch.Tensor:
+                out_nchw=False, cout: Optional[int] = None, out_f32=False) -> torch.Tensor:
     """Channels-last implicit-GEMM conv.  x [N,H,W,Ca] (+ x_b [N,H,W,Cb] concatenated),
     optional fused 1x1 shortcut over concat(shortcut, shortcut_b), weight from
-    ``pack_conv_weight`` (segment-1 columns appended)."""
+    ``pack_conv_weight`` (segment-1 columns appended).  The residual may be
+    fp16 or fp32; out_f32 gives an fp32 output."""
     N, H, W, Ca = x.shape
     Cb = 0 if x_b is None else x_b.shape[3]
     C1a = 0 if shortcut is None else shortcut.shape[3]
@@ -363,11 +403,14 @@ def conv2d_nhwc(x: torch.Tensor, w_packed: torch.Tensor, *, KH: int, KW: int, st
     _need(w_packed, Cout * w_packed.shape[1], "w_packed")
     _need(bias, Cout, "bias", optional=True)
     _need(tbias, N * Cout, "tbias", optional=True)
-    _need(residual, N * Ho * Wo * Cout, "residual", optional=True)
+    res_f32 = residual is not None and residual.dtype == torch.float32
+    _need(residual, N * Ho * Wo * Cout, "residual", optional=True,
+          dtype=torch.float32 if res_f32 else torch.float16)
+    odt = torch.float32 if out_f32 else torch.float16
     if out is None:
         shape = (N, Cout, Ho, Wo) if out_nchw else (N, Ho, Wo, Cout)
-        out = torch.empty(shape, dtype=torch.float16, device=x.device)
-    _need(out, N * Ho * Wo * Cout, "out")
+        out = torch.empty(shape, dtype=odt, device=x.device)
+    _need(out, N * Ho * Wo * Cout, "out", dtype=odt)
     a = ConvNhwcArgs()
     a.src0a, a.src0b, a.C0a, a.C0b, a.ld0a, a.ld0b = _p(x), _p(x_b), Ca, Cb, Ca, max(Cb, 0)
     a.src1a, a.src1b, a.C1a, a.C1b, a.ld1a, a.ld1b = _p(shortcut), _p(shortcut_b), C1a, C1b, C1a, C1b
@@ -376,6 +419,7 @@ def conv2d_nhwc(x: torch.Tensor, w_packed: torch.Tensor, *, KH: int, KW: int, st
     a.bias, a.tbias, a.tbias_ld = _p(bias), _p(tbias), Cout
     a.residual, a.res_ld = _p(residual), Cout
     a.out, a.ldy, a.out_nchw, a.act = _p(out), Cout, int(out_nchw), int(act)
+    a.out_f32, a.res_f32 = int(out_f32), int(res_f32)
     call("dlm_conv2d_nhwc_fp16", ctypes.byref(a), stream_handle())
     return out
 
@@ -390,7 +434,7 @@ def group_norm_nhwc(x: torch.Tensor, gamma, beta, groups: int, eps: float, silu:
     Cb = 0 if x_b is None else x_b.shape[3]
     C = Ca + Cb
     HW = H * W
-    _need(x, N * HW * Ca, "x")
+    _need(x, N * HW * Ca, "x", dtype=x.dtype if x.dtype == torch.float32 else torch.float16)
     _need(x_b, N * HW * Cb, "x_b", optional=True)
     _need(gamma, C, "gamma", optional=True)
     _need(beta, C, "beta", optional=True)
@@ -402,6 +446,12 @@ def group_norm_nhwc(x: torch.Tensor, gamma, beta, groups: int, eps: float, silu:
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         _ws_cache[x.device] = ws
+    if x.dtype == torch.float32:
+        if x_b is not None:
+            raise ValueError("fp32 GroupNorm takes one source")
+        call("dlm_group_norm_nhwc_f32in", _p(x), C, _p(gamma), _p(beta), _p(out), C, N, HW, C,
+             groups, float(eps), int(silu), _p(ws), stream_handle())
+        return out
     call("dlm_group_norm_nhwc_fp16", _p(x), Ca, Ca, _p(x_b), max(Cb, 8), _p(gamma), _p(beta),
          _p(out), C, N, HW, C, groups, float(eps), int(silu), _p(ws), stream_handle())
     return out

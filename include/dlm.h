@@ -195,6 +195,16 @@ int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const voi
                        int ldy, void* VT, int vt_col0, int tokens, int vt_ld, int M, int N, int K,
                        void* stream);
 
+/* dlm_linear_fp16 with an fp32 output Y and an fp32 residual R (fp16 X, W,
+ * bias; act none/silu/gelu): Y = act(alpha * X W^T + bias) + beta * R.  Used
+ * where a result leaves the fp16 range or feeds a softmax: the VAE mid-block
+ * attention scores (the reference computes them inside launch_attention,
+ * src/kernels/vae_decode.cu:682-683) and the decoder's fp32 stages
+ * (src/kernels/vae_decode.cu:317-327). */
+int dlm_linear_f32out_fp16(const void* X, int lda, const void* W, int ldw, const void* bias,
+                           const float* R, int ldr, float* Y, int ldy, int M, int N, int K,
+                           float alpha, float beta, int act, void* stream);
+
 /* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
  * diffusers stores them) into the 32-row interleave DLM_ACT_GEGLU expects
  * (d % 32 == 0). */
@@ -233,7 +243,9 @@ int dlm_nhwc_to_nchw_fp16(const void* in, void* out, int N, int C, int HW, int C
  * (the fused ResnetBlock2D conv_shortcut).  Weight rows are [Cout, Ktot] with
  * Ktot = KH*KW*(C0a+C0b) + (C1a+C1b), channels-last per tap (see
  * dlm_conv_weight_pack_fp16), row stride ldw.  Output channels-last with row
- * stride ldy, or NCHW when out_nchw = 1. */
+ * stride ldy, or NCHW when out_nchw = 1; fp32 output elements when
+ * out_f32 = 1 and an fp32 residual when res_f32 = 1 (the VAE decoder's fp32
+ * stages, src/kernels/vae_decode.cu:317-327; operands stay fp16). */
 typedef struct dlm_conv_nhwc_args {
   const void* src0a; const void* src0b; int C0a; int C0b; int ld0a; int ld0b;
   const void* src1a; const void* src1b; int C1a; int C1b; int ld1a; int ld1b;
@@ -242,6 +254,8 @@ typedef struct dlm_conv_nhwc_args {
   const void* bias; const void* tbias; int tbias_ld;
   const void* residual; int res_ld;
   void* out; int ldy; int out_nchw; int act;
+  int out_f32;  /* 1: out holds fp32 elements */
+  int res_f32;  /* 1: residual holds fp32 elements */
 } dlm_conv_nhwc_args;
 int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* args, void* stream);
 
@@ -255,6 +269,12 @@ int dlm_group_norm_nhwc_fp16(const void* in_a, int C_a, int ld_a, const void* in
                              const void* gamma, const void* beta, void* out, int ld_out,
                              int N, int HW, int C, int num_groups, float eps, int fuse_silu,
                              void* workspace, void* stream);
+/* Same GroupNorm(+SiLU) over fp32 channels-last input (one source), fp16
+ * output: the VAE decoder's fp32 stages (reference launch_group_norm_f32,
+ * src/kernels/vae_decode.cu:466-545). */
+int dlm_group_norm_nhwc_f32in(const float* in, int ld_in, const void* gamma, const void* beta,
+                              void* out, int ld_out, int N, int HW, int C, int num_groups,
+                              float eps, int fuse_silu, void* workspace, void* stream);
 
 /* Strided flash attention: element (b, s, h, d) of Q is at
  * q[b*q_sb + s*q_ss + h*q_sh + d] (likewise K, V, O); Dh = 64. */
@@ -325,6 +345,31 @@ int dlm_euler_cfg_step(float* latent, const void* noise, void* model_in, int n,
  * step's scale_model_input, reference src/infer/scheduler.hpp:112-120). */
 int dlm_scale_latent_fp16(const float* latent, void* model_in, int n, float scale, int copies,
                           void* stream);
+
+/* ------------------------------------------------------------------ */
+/* VAE decoder helpers                                                 */
+/* ------------------------------------------------------------------ */
+
+/* out[i] = fp16(in[i] * scale) (reference k_f2h, src/kernels/vae_decode.cu:
+ * 340-347, with a power-of-two scale that keeps an fp32 activation inside
+ * the fp16 range when it becomes a conv operand). */
+int dlm_cast_f32_to_f16(const float* in, void* out, long long n, float scale, void* stream);
+/* x[i] = fp16(x[i] * scale) in place. */
+int dlm_scale_fp16(void* x, long long n, float scale, void* stream);
+/* out[i] = fp16(latent[i] / scaling_factor): the VAE input (reference
+ * src/infer/diffusion.cu:980-984; SDXL scaling_factor 0.13025). */
+int dlm_latent_to_vae_fp16(const float* latent, void* out, long long n, float scaling_factor,
+                           void* stream);
+/* Decoded image [N, 3, H, W] fp16 in [-1, 1] -> device RGB8 [N, H, W, 3]
+ * with q = int(clamp(v/2 + 1/2, 0, 1) * 255 + 0.5) (reference
+ * image_f16_to_rgb_u8, src/infer/diffusion.cu:146-165); NaN -> 0. */
+int dlm_image_to_rgb8(const void* image, uint8_t* rgb, int N, int H, int W, void* stream);
+/* P[r, :] = softmax(S[r, :]) for fp32 scores S [rows, cols] (row stride
+ * lds) into fp16 P (row stride ldp); cols, lds, ldp multiples of 4.  The
+ * softmax step of the VAE mid-block attention (reference launch_attention
+ * with Dh = 512, src/kernels/vae_decode.cu:682-683). */
+int dlm_softmax_rows_f32_fp16(const float* S, long long lds, void* P, long long ldp, int rows,
+                              int cols, void* stream);
 
 #ifdef __cplusplus
 }

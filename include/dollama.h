@@ -128,6 +128,57 @@ int dlm_pipeline_denoise(void* unet, int steps, float guidance, int H, int W, fl
                          const void* ehs, int ctx_len, const void* text, const void* time_ids,
                          void* stream);
 
+/* ------------------------------------------------------------------ */
+/* SDXL VAE decoder (AutoencoderKL decoder + post_quant_conv)          */
+/* ------------------------------------------------------------------ */
+
+typedef struct dlm_vae_config {
+  int ch[4];            /* block_out_channels, encoder order (SDXL 128, 256, 512, 512) */
+  int latent_channels;  /* 4 */
+  int out_channels;     /* 3 */
+  int layers;           /* resnets per decoder up block (3) */
+  int groups;           /* GroupNorm groups (32) */
+  int fp32_from;        /* decoder up blocks >= this keep fp32 activations (2) */
+} dlm_vae_config;
+
+int dlm_vae_config_sdxl(dlm_vae_config* cfg);
+int dlm_vae_weight_count(const dlm_vae_config* cfg, int* count);
+int dlm_vae_weight_spec(const dlm_vae_config* cfg, int index, char* name, int name_len,
+                        int* ndim, int64_t* shape /* [4] */);
+
+/* Resident weight handle (replaces vae_weights_create / vae_weights_destroy,
+ * src/kernels/vae_decode.cuh:59-69): set_weight registers fp16 device
+ * buffers (decoder.* and post_quant_conv.* diffusers names, borrowed until
+ * prepare), prepare packs them into the handle's own memory. */
+int dlm_vae_create(const dlm_vae_config* cfg, void** handle);
+int dlm_vae_destroy(void* handle);
+int dlm_vae_set_weight(void* handle, const char* name, const void* dptr, int ndim,
+                       const int64_t* shape);
+int dlm_vae_load_safetensors(void* handle, const char* path, void* stream);
+int dlm_vae_prepare(void* handle, void* stream);
+int dlm_vae_packed_bytes(void* handle, size_t* bytes);
+
+/* image [N, out_channels, 8h, 8w] fp16 NCHW (values in about [-1, 1]) from
+ * latent [N, latent_channels, h, w] fp16 NCHW already divided by the scaling
+ * factor (dlm_latent_to_vae_fp16); h * w a multiple of 8, 1 <= N <= 16.
+ * Replaces launch_vae_decode(handle, d_latent, d_image_out)
+ * (src/kernels/vae_decode.cuh:71-75), which decodes one 128x128 latent and
+ * synchronises; this call is stream-ordered. */
+int dlm_vae_decode(void* handle, int N, int h, int w, const void* latent, void* image,
+                   void* stream);
+
+/* Stage hook for tests (the reference's golden stages, src/tests/
+ * test_vae_decode.cu): post_quant_conv_out (8 channels, the last 4 zero),
+ * conv_in_out, mid_block_out, up_block_{0..3}_out (channels-last, fp32
+ * when is_f32), final_image (NCHW fp16). */
+typedef void (*dlm_vae_stage_hook)(const char* name, const void* dptr, size_t n, int C,
+                                   int is_f32, void* user);
+int dlm_vae_set_stage_hook(void* handle, dlm_vae_stage_hook hook, void* user);
+/* Kernel timing by class: 0 conv, 1 linear, 2 attention, 3 groupnorm,
+ * 4 other; out[4*c + 0..3] as dlm_unet_profile_report. */
+int dlm_vae_set_profiling(void* handle, int on);
+int dlm_vae_profile_report(void* handle, double* out /* [20] */, void* stream);
+
 /* VRAM arena statistics (src/kernels/device_arena.cuh DeviceArenaStats):
  * out[0..10] = cuda_malloc_calls, cuda_free_calls, chunk_alloc_calls,
  * alloc_calls, total_capacity, live_chunks, bytes_in_use, peak_bytes_in_use,

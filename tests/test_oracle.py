@@ -324,3 +324,102 @@ def test_small_unet_forward_runs_and_is_deterministic():
     b = OR.unet_forward(W, OR.TINY, lat, torch.tensor([999.0]), ehs, text, ids)
     assert torch.isfinite(a).all() and torch.equal(a, b) and a.shape == (1, 4, 16, 16)
     assert len(stages) >= 10
+
+
+# ------------------------------------------------------------------ VAE --
+def test_vae_param_count_is_the_published_autoencoder_total():
+    """Decoder + post_quant_conv list of the oracle plus the encoder +
+    quant_conv of the same architecture (counted here from the diffusers
+    AutoencoderKL layout) = 83,653,863, the published parameter count of the
+    SD / SDXL AutoencoderKL."""
+    from oracle import vae_ref as OV
+    dec = sum(math.prod(s) for s in OV.param_shapes(OV.SDXL_VAE).values())
+
+    def conv(o, i, k):
+        return o * i * k * k + o
+
+    def res(i, o):
+        return 2 * i + conv(o, i, 3) + 2 * o + conv(o, o, 3) + (conv(o, i, 1) if i != o else 0)
+
+    enc, cin = conv(128, 3, 3), 128
+    for b, co in enumerate((128, 256, 512, 512)):
+        enc += res(cin, co) + res(co, co) + (conv(co, co, 3) if b < 3 else 0)
+        cin = co
+    enc += 2 * res(512, 512) + 2 * 512 + 4 * (512 * 512 + 512)  # mid: 2 resnets + attention
+    enc += 2 * 512 + conv(8, 512, 3) + conv(8, 8, 1)  # norm_out, conv_out, quant_conv
+    assert dec == 49_490_199
+    assert dec + enc == 83_653_863
+
+
+def _vae_skeleton_weights(cfg, seed):
+    """Weights under which every resnet and the attention are identities
+    (conv2, to_out and their biases zero; shortcuts select the first Co
+    channels) and every upsampler conv is the identity kernel."""
+    from oracle import vae_ref as OV
+    W = OV.random_weights(cfg, seed)
+    for k, v in W.items():
+        if ".conv2." in k or ".to_out.0." in k:
+            W[k] = torch.zeros_like(v)
+        elif ".conv_shortcut.weight" in k:
+            o, i = v.shape[:2]
+            W[k] = torch.eye(o, i)[:, :, None, None].contiguous()
+        elif ".conv_shortcut.bias" in k:
+            W[k] = torch.zeros_like(v)
+        elif ".upsamplers.0.conv.weight" in k:
+            o = v.shape[0]
+            t = torch.zeros_like(v)
+            t[:, :, 1, 1] = torch.eye(o)
+            W[k] = t
+        elif ".upsamplers.0.conv.bias" in k:
+            W[k] = torch.zeros_like(v)
+    return W
+
+
+def test_vae_decoder_reduces_to_upsampled_head():
+    """With identity resnets / attention / upsamplers the decoder must equal
+    conv_out(silu(GN(nearest_8x(first C3 channels of conv_in(pqc(z)))))),
+    computed here with library calls only; this fixes the number and order
+    of the upsamples, the residual wiring and the channel flow."""
+    import torch.nn.functional as F
+    from oracle import vae_ref as OV
+    cfg = OV.TINY_VAE
+    W = _vae_skeleton_weights(cfg, 5)
+    z = _rand((2, 4, 6, 5), 6)
+    got = OV.vae_decode(W, cfg, z)
+    c3 = OV.decoder_channels(cfg)[3]
+    x = F.conv2d(z, W["post_quant_conv.weight"], W["post_quant_conv.bias"])
+    x = F.conv2d(x, W["decoder.conv_in.weight"], W["decoder.conv_in.bias"], padding=1)
+    x = F.interpolate(x[:, :c3], scale_factor=8, mode="nearest")
+    x = F.silu(F.group_norm(x, 32, W["decoder.conv_norm_out.weight"], W["decoder.conv_norm_out.bias"], 1e-6))
+    ref = F.conv2d(x, W["decoder.conv_out.weight"], W["decoder.conv_out.bias"], padding=1)
+    assert got.shape == (2, 3, 48, 40)
+    _close(got, ref, 1e-4)
+
+
+def test_vae_attention_block_is_single_head_sdpa():
+    """The mid-block attention equals torch's scaled_dot_product_attention
+    (one head, default scale 1/sqrt(C)) between the same projections."""
+    import torch.nn.functional as F
+    from oracle import vae_ref as OV
+    W = OV.random_weights(OV.TINY_VAE, 7)
+    C = OV.decoder_channels(OV.TINY_VAE)[0]
+    x = _rand((1, C, 6, 7), 8)
+    p = "decoder.mid_block.attentions.0."
+    got = OV.attn_block(W, p, x)
+    h = F.group_norm(x, 32, W[p + "group_norm.weight"], W[p + "group_norm.bias"], 1e-6)
+    h = h.flatten(2).transpose(1, 2)
+    q, k, v = (F.linear(h, W[p + n + ".weight"], W[p + n + ".bias"]) for n in ("to_q", "to_k", "to_v"))
+    o = F.scaled_dot_product_attention(q[:, None], k[:, None], v[:, None])[:, 0]
+    o = F.linear(o, W[p + "to_out.0.weight"], W[p + "to_out.0.bias"])
+    _close(got, x + o.transpose(1, 2).reshape(x.shape), 1e-4)
+
+
+def test_rgb8_fixed_points():
+    """-1 -> 0, 1 -> 255, 0 -> int(127.5 + 0.5) = 128, clamping beyond [-1, 1],
+    HWC order (src/infer/diffusion.cu:146-165)."""
+    from oracle import vae_ref as OV
+    img = torch.tensor([-1.0, 1.0, 0.0, -3.0, 3.0, 0.5]).reshape(1, 3, 1, 2)
+    q = OV.image_to_rgb8(img)
+    assert q.shape == (1, 1, 2, 3)
+    # channel planes [-1, 1], [0, -3], [3, 0.5] -> pixels (-1, 0, 3) and (1, -3, 0.5)
+    assert q[0, 0, 0].tolist() == [0, 128, 255] and q[0, 0, 1].tolist() == [255, 0, 191]
