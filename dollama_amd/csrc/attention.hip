@@ -492,7 +492,6 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   // One 32-query block per wave: the softmax is VALU work that only other
   // waves' MFMAs can hide, so more waves beat sharing K/V fragments between
   // two query blocks (2x4096^2 x10 heads: 144 us vs 170 us).
-  const long long wg2 = (long long)((a->Sq + 255) / 256) * a->H * a->B;
   const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
   hipLaunchKernelGGL(flash_vt_pipe_kernel, grid, dim3(256), 0, s, p);
   DLM_LAUNCH_CHECK();

@@ -171,6 +171,17 @@ __global__ void euler_cfg_kernel(float* latent, const f16* noise, f16* model_in,
   }
 }
 
+// Euler step without guidance (one noise prediction, the reference's
+// generate() path, src/infer/diffusion.cu:650-660 + scheduler.hpp step).
+__global__ void euler_kernel(float* latent, const f16* noise, f16* model_in, int n, float dt,
+                             float in_scale) {
+  GRID_STRIDE(i, n) {
+    const float x = latent[i] + (float)noise[i] * dt;
+    latent[i] = x;
+    model_in[i] = (f16)(x * in_scale);
+  }
+}
+
 __global__ void scale_latent_kernel(const float* latent, f16* model_in, int n, float scale,
                                     int copies) {
   GRID_STRIDE(i, n) {
@@ -370,6 +381,16 @@ int dlm_euler_cfg_step(float* latent, const void* noise, void* model_in, int n, 
   hipLaunchKernelGGL(euler_cfg_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      latent, (const f16*)noise, (f16*)model_in, n, guidance, sigma_next - sigma,
                      in_scale);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_euler_step(float* latent, const void* noise, void* model_in, int n, float sigma,
+                   float sigma_next, float in_scale, void* stream) {
+  if (n <= 0) return DLM_OK;
+  DLM_REQUIRE(latent && noise && model_in, "NULL pointer");
+  hipLaunchKernelGGL(euler_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, latent,
+                     (const f16*)noise, (f16*)model_in, n, sigma_next - sigma, in_scale);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

@@ -12,6 +12,7 @@
 #include "device_arena.hpp"
 #include "lora.hpp"
 #include "pipeline.hpp"
+#include "runner.hpp"
 #include "safetensors.hpp"
 #include "scheduler.hpp"
 #include "unet.hpp"
@@ -35,6 +36,8 @@ int guarded(F&& f) {
     return guard_status(e, DLM_ERR_INVALID_ARG);
   } catch (const std::bad_alloc& e) {
     return guard_status(e, DLM_ERR_OUT_OF_MEMORY);
+  } catch (const std::out_of_range& e) {
+    return guard_status(e, DLM_ERR_NOT_FOUND);
   } catch (const std::exception& e) {
     return guard_status(e, DLM_ERR_STATE);
   }
@@ -162,21 +165,7 @@ int dlm_unet_prepare(void* handle, void* stream) {
 int dlm_unet_load_safetensors(void* handle, const char* path, void* stream) {
   return guarded([&] {
     if (!handle || !path) throw std::invalid_argument("NULL argument");
-    UNet* u = static_cast<UNet*>(handle);
-    SafeTensors st(path);
-    // one upload of the whole data region, tensors registered in place
-    void* dev = nullptr;
-    DLM_CALL(dlm_malloc(&dev, st.data_bytes()));
-    std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
-    DLM_CALL(dlm_memcpy(dev, st.data(), st.data_bytes(), 0));
-    for (const WeightSpec& s : unet_weight_specs(u->config())) {
-      if (!st.has(s.name)) throw std::runtime_error("safetensors: missing '" + s.name + "'");
-      if (st.dtype(s.name) != StDtype::F16)
-        throw std::runtime_error("safetensors: '" + s.name + "' is not F16");
-      if (st.offset(s.name) % 2 != 0) throw std::runtime_error("safetensors: misaligned tensor");
-      u->set_weight(s.name, static_cast<char*>(dev) + st.offset(s.name), st.shape(s.name));
-    }
-    u->prepare(stream);
+    load_unet_safetensors(*static_cast<UNet*>(handle), path, stream);
   });
 }
 
@@ -199,20 +188,8 @@ static void fill_counts(int* counts, const LoraReport& r) {
 int dlm_unet_load_lora(void* handle, const char* path, float strength, int* counts, void* stream) {
   return guarded([&] {
     if (!handle || !path) throw std::invalid_argument("NULL argument");
-    UNet* u = static_cast<UNet*>(handle);
-    SafeTensors st(path);
     LoraReport rep;
-    std::vector<LoraModule> mods = load_lora_modules(unet_weight_specs(u->config()), st, strength, &rep);
-    for (const LoraModule& m : mods) {
-      void* dev = nullptr;
-      const size_t na = m.a_fp16.size(), nb = m.b_fp16.size();
-      DLM_CALL(dlm_malloc(&dev, (na + nb) * 2));
-      std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
-      DLM_CALL(dlm_memcpy(dev, m.a_fp16.data(), na * 2, 0));
-      DLM_CALL(dlm_memcpy(static_cast<uint16_t*>(dev) + na, m.b_fp16.data(), nb * 2, 0));
-      u->apply_lora(m.base_key, dev, static_cast<uint16_t*>(dev) + na, m.rank, m.in_flat, m.out_dim,
-                    m.scale, stream);
-    }
+    unet_apply_lora_file(*static_cast<UNet*>(handle), path, strength, &rep, stream);
     fill_counts(counts, rep);
   });
 }
@@ -385,20 +362,7 @@ int dlm_vae_prepare(void* handle, void* stream) {
 int dlm_vae_load_safetensors(void* handle, const char* path, void* stream) {
   return guarded([&] {
     if (!handle || !path) throw std::invalid_argument("NULL argument");
-    VAE* v = static_cast<VAE*>(handle);
-    SafeTensors st(path);
-    void* dev = nullptr;
-    DLM_CALL(dlm_malloc(&dev, st.data_bytes()));
-    std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
-    DLM_CALL(dlm_memcpy(dev, st.data(), st.data_bytes(), 0));
-    for (const WeightSpec& s : vae_weight_specs(v->config())) {
-      if (!st.has(s.name)) throw std::runtime_error("safetensors: missing '" + s.name + "'");
-      if (st.dtype(s.name) != StDtype::F16)
-        throw std::runtime_error("safetensors: '" + s.name + "' is not F16");
-      if (st.offset(s.name) % 2 != 0) throw std::runtime_error("safetensors: misaligned tensor");
-      v->set_weight(s.name, static_cast<char*>(dev) + st.offset(s.name), st.shape(s.name));
-    }
-    v->prepare(stream);
+    load_vae_safetensors(*static_cast<VAE*>(handle), path, stream);
   });
 }
 
@@ -440,6 +404,154 @@ int dlm_vae_profile_report(void* handle, double* out, void* stream) {
       out[4 * c + 2] = r[c].flops;
       out[4 * c + 3] = r[c].bytes;
     }
+  });
+}
+
+// ------------------------------------------------------------------ runner / backend
+
+static void copy_rgb(const std::vector<uint8_t>& rgb, uint8_t* out, size_t cap) {
+  if (rgb.size() > cap) throw std::invalid_argument("rgb_out holds " + std::to_string(cap) +
+                                                    " bytes, the image needs " + std::to_string(rgb.size()));
+  std::memcpy(out, rgb.data(), rgb.size());
+}
+
+int dlm_runner_create(const char* unet_weights, const char* vae_weights, const char* embeds,
+                      float vae_scaling_factor, const dlm_unet_config* ucfg, const dlm_vae_config* vcfg,
+                      int latent_h, int latent_w, void** handle) {
+  return guarded([&] {
+    if (!unet_weights || !vae_weights || !embeds || !handle) throw std::invalid_argument("NULL argument");
+    *handle = nullptr;
+    std::unique_ptr<IDiffusionRunner> r = make_diffusion_runner(
+        unet_weights, vae_weights, embeds, FastConfig{}, vae_scaling_factor,
+        ucfg ? to_cfg(ucfg) : UNetConfig{}, vcfg ? to_vcfg(vcfg) : VaeConfig{}, latent_h, latent_w);
+    if (!r) throw std::runtime_error("make_diffusion_runner returned no runner (see stderr)");
+    *handle = r.release();
+  });
+}
+
+int dlm_runner_destroy(void* handle) {
+  return guarded([&] { delete static_cast<IDiffusionRunner*>(handle); });
+}
+
+int dlm_runner_txt2img(void* handle, int steps, uint64_t seed, float guidance, const float* cond_ehs,
+                       const float* cond_text, const float* uncond_ehs, const float* uncond_text,
+                       const float* time_ids, uint8_t* rgb_out, size_t rgb_capacity, int* w, int* h) {
+  return guarded([&] {
+    if (!handle || !rgb_out || !w || !h) throw std::invalid_argument("NULL argument");
+    std::vector<uint8_t> rgb;
+    static_cast<IDiffusionRunner*>(handle)->run_txt2img(steps, seed, guidance, cond_ehs, cond_text,
+                                                        uncond_ehs, uncond_text, time_ids, rgb, *w, *h);
+    copy_rgb(rgb, rgb_out, rgb_capacity);
+  });
+}
+
+int dlm_runner_generate(void* handle, int steps, uint64_t seed, uint8_t* rgb_out, size_t rgb_capacity,
+                        int* w, int* h) {
+  return guarded([&] {
+    if (!handle || !rgb_out || !w || !h) throw std::invalid_argument("NULL argument");
+    auto* r = dynamic_cast<DiffusionRunner*>(static_cast<IDiffusionRunner*>(handle));
+    if (!r) throw std::invalid_argument("not a DiffusionRunner handle");
+    std::vector<uint8_t> rgb;
+    r->pipeline().generate(steps, seed, 1.0f, rgb, *w, *h);
+    copy_rgb(rgb, rgb_out, rgb_capacity);
+  });
+}
+
+int dlm_runner_apply_loras(void* handle, const char* const* paths, const float* strengths, int n) {
+  return guarded([&] {
+    if (!handle || n < 0 || (n > 0 && (!paths || !strengths))) throw std::invalid_argument("bad argument");
+    std::vector<LoraFileRequest> reqs;
+    for (int i = 0; i < n; ++i) reqs.push_back(LoraFileRequest{paths[i], strengths[i]});
+    static_cast<IDiffusionRunner*>(handle)->apply_loras(reqs);
+  });
+}
+
+int dlm_runner_clear_loras(void* handle) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<IDiffusionRunner*>(handle)->clear_loras();
+  });
+}
+
+int dlm_backend_create(const dlm_backend_config* c, void** handle) {
+  return guarded([&] {
+    if (!c || !handle || !c->backend_name) throw std::invalid_argument("NULL argument");
+    *handle = nullptr;
+    BackendConfig b;
+    b.backend_name = c->backend_name;
+    b.preset = c->preset ? c->preset : "";
+    b.unet_weights = c->unet_weights ? c->unet_weights : "";
+    b.vae_weights = c->vae_weights ? c->vae_weights : "";
+    b.embeds = c->embeds ? c->embeds : "";
+    b.vae_scaling_factor = c->vae_scaling_factor;
+    if (c->unet_cfg) b.unet_cfg = to_cfg(c->unet_cfg);
+    if (c->vae_cfg) b.vae_cfg = to_vcfg(c->vae_cfg);
+    if (c->latent_size > 0) b.latent_size = c->latent_size;
+    std::unique_ptr<IDiffusionBackend> be = make_backend(b);
+    if (!be) throw std::out_of_range("make_backend: no backend for '" + b.backend_name + "' (see stderr)");
+    *handle = be.release();
+  });
+}
+
+int dlm_backend_destroy(void* handle) {
+  return guarded([&] { delete static_cast<IDiffusionBackend*>(handle); });
+}
+
+int dlm_backend_generate(void* handle, const char* prompt, const char* negative, int steps, uint64_t seed,
+                         float cfg, int w, int h, uint8_t* rgb_out, size_t rgb_capacity, int* w_out,
+                         int* h_out) {
+  return guarded([&] {
+    if (!handle || !rgb_out || !w_out || !h_out) throw std::invalid_argument("NULL argument");
+    std::vector<uint8_t> rgb;
+    static_cast<IDiffusionBackend*>(handle)->generate(prompt ? prompt : "", negative ? negative : "", steps,
+                                                      seed, cfg, w, h, rgb, *w_out, *h_out);
+    copy_rgb(rgb, rgb_out, rgb_capacity);
+  });
+}
+
+int dlm_backend_info(void* handle, char* name, int name_len, int* latent_channels, int* native_resolution,
+                     int* needs_t5) {
+  return guarded([&] {
+    if (!handle || !name || name_len <= 0 || !latent_channels || !native_resolution || !needs_t5)
+      throw std::invalid_argument("NULL argument");
+    const BackendInfo i = static_cast<IDiffusionBackend*>(handle)->info();
+    if ((int)i.name.size() >= name_len) throw std::invalid_argument("name buffer too small");
+    std::memcpy(name, i.name.c_str(), i.name.size() + 1);
+    *latent_channels = i.latent_channels;
+    *native_resolution = i.native_resolution;
+    *needs_t5 = i.needs_t5 ? 1 : 0;
+  });
+}
+
+int dlm_backend_model_id(void* handle, char* buf, int len) {
+  return guarded([&] {
+    if (!handle || !buf || len <= 0) throw std::invalid_argument("NULL argument");
+    const std::string id = static_cast<IDiffusionBackend*>(handle)->model_id();
+    if ((int)id.size() >= len) throw std::invalid_argument("buffer too small");
+    std::memcpy(buf, id.c_str(), id.size() + 1);
+  });
+}
+
+int dlm_backend_apply_loras(void* handle, const char* const* names, const float* strengths, int n) {
+  return guarded([&] {
+    if (!handle || n < 0 || (n > 0 && (!names || !strengths))) throw std::invalid_argument("bad argument");
+    std::vector<LoraRequest> reqs;
+    for (int i = 0; i < n; ++i) reqs.push_back(LoraRequest{names[i], strengths[i]});
+    static_cast<IDiffusionBackend*>(handle)->apply_loras(reqs);
+  });
+}
+
+int dlm_backend_clear_loras(void* handle) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<IDiffusionBackend*>(handle)->clear_loras();
+  });
+}
+
+int dlm_randn_latent(uint64_t seed, double sigma0, float* out, size_t n) {
+  return guarded([&] {
+    if (!out && n) throw std::invalid_argument("NULL out");
+    randn_latent(seed, sigma0, out, n);
   });
 }
 

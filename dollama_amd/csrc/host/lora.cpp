@@ -2,7 +2,10 @@
 
 #include <cstring>
 #include <map>
+#include <memory>
 #include <stdexcept>
+
+#include "check.hpp"
 
 namespace dollama {
 
@@ -188,6 +191,24 @@ std::vector<LoraModule> load_lora_modules(const std::vector<WeightSpec>& base,
   rep.modules = mods.size();
   if (report) *report = rep;
   return mods;
+}
+
+void unet_apply_lora_file(UNet& u, const std::string& path, float strength, LoraReport* report,
+                          void* stream) {
+  SafeTensors st(path);
+  LoraReport rep;
+  const std::vector<LoraModule> mods = load_lora_modules(unet_weight_specs(u.config()), st, strength, &rep);
+  for (const LoraModule& m : mods) {
+    void* dev = nullptr;
+    const size_t na = m.a_fp16.size(), nb = m.b_fp16.size();
+    DLM_CALL(dlm_malloc(&dev, (na + nb) * 2));
+    std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
+    DLM_CALL(dlm_memcpy(dev, m.a_fp16.data(), na * 2, 0));
+    DLM_CALL(dlm_memcpy(static_cast<uint16_t*>(dev) + na, m.b_fp16.data(), nb * 2, 0));
+    u.apply_lora(m.base_key, dev, static_cast<uint16_t*>(dev) + na, m.rank, m.in_flat, m.out_dim, m.scale,
+                 stream);
+  }
+  if (report) *report = rep;
 }
 
 }  // namespace dollama

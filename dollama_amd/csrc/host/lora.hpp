@@ -44,4 +44,10 @@ std::vector<LoraModule> load_lora_modules(const std::vector<WeightSpec>& base,
 
 uint16_t f32_to_f16_rne(float v);
 
+// Load a LoRA file and merge every UNet module into the resident weights
+// (reference DiffusionPipeline::apply_lora_file, src/infer/diffusion.cu).
+// Modules applied before a failing one stay applied.
+void unet_apply_lora_file(UNet& u, const std::string& path, float strength, LoraReport* report,
+                          void* stream);
+
 }  // namespace dollama

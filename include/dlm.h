@@ -341,6 +341,12 @@ int dlm_euler_cfg_step(float* latent, const void* noise, void* model_in, int n,
                        float guidance, float sigma, float sigma_next, float in_scale,
                        void* stream);
 
+/* Euler step without guidance (one noise prediction [n]): latent +=
+ * noise * (sigma_next - sigma) in fp32, model_in[0:n] = fp16(latent *
+ * in_scale) (reference generate(), src/infer/diffusion.cu:551-680). */
+int dlm_euler_step(float* latent, const void* noise, void* model_in, int n, float sigma,
+                   float sigma_next, float in_scale, void* stream);
+
 /* model_in[c*n + i] = fp16(latent[i] * scale) for c < copies (the first
  * step's scale_model_input, reference src/infer/scheduler.hpp:112-120). */
 int dlm_scale_latent_fp16(const float* latent, void* model_in, int n, float scale, int copies,

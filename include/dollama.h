@@ -179,6 +179,79 @@ int dlm_vae_set_stage_hook(void* handle, dlm_vae_stage_hook hook, void* user);
 int dlm_vae_set_profiling(void* handle, int on);
 int dlm_vae_profile_report(void* handle, double* out /* [20] */, void* stream);
 
+/* ------------------------------------------------------------------ */
+/* Text-to-image runner and backend plugin                             */
+/* ------------------------------------------------------------------ */
+
+/* IDiffusionRunner over the device pipeline (reference make_diffusion_runner
+ * + DiffusionRunner, src/server/diffusion_runner.hpp:33-79 and
+ * diffusion_runner.cu:33-160).  Loads the UNet and VAE safetensors (diffusers
+ * keys) and the embeddings file (input_encoder_hidden_states_f16,
+ * input_text_embeds_f16, input_time_ids_f16; src/infer/diffusion.cu:305-312).
+ * ucfg / vcfg NULL = SDXL; latent 128 x 128 = a 1024 x 1024 image.  Where the
+ * reference returns nullptr (unreadable file, failed construction) this
+ * returns a non-zero status and *handle = NULL.  An invalid
+ * vae_scaling_factor (<= 0 or not finite) falls back to 0.13025. */
+int dlm_runner_create(const char* unet_weights, const char* vae_weights, const char* embeds,
+                      float vae_scaling_factor, const dlm_unet_config* ucfg,
+                      const dlm_vae_config* vcfg, int latent_h, int latent_w, void** handle);
+int dlm_runner_destroy(void* handle);
+/* run_txt2img: CFG with guidance, host fp32 conditioning (ehs [ctx_len *
+ * cross_dim], text [text_dim], time_ids [6]); the seed gives the reference's
+ * initial latent (dlm_randn_latent); rgb_out receives [h, w, 3] bytes
+ * (rgb_capacity >= 3 * w * h). */
+int dlm_runner_txt2img(void* handle, int steps, uint64_t seed, float guidance,
+                       const float* cond_ehs, const float* cond_text, const float* uncond_ehs,
+                       const float* uncond_text, const float* time_ids, uint8_t* rgb_out,
+                       size_t rgb_capacity, int* w, int* h);
+/* DiffusionPipeline::generate (guidance 1, conditioning from the embeddings
+ * file, B=1 forwards; src/infer/diffusion.cu:551-700). */
+int dlm_runner_generate(void* handle, int steps, uint64_t seed, uint8_t* rgb_out,
+                        size_t rgb_capacity, int* w, int* h);
+/* Apply LoRA files in order; on any failure every LoRA is cleared and the
+ * error returned (reference DiffusionRunner::apply_loras). */
+int dlm_runner_apply_loras(void* handle, const char* const* paths, const float* strengths, int n);
+int dlm_runner_clear_loras(void* handle);
+
+/* IDiffusionBackend registry (reference make_backend,
+ * src/server/diffusion_backend.cpp): backend_name "sdxl" builds the SDXL
+ * backend; any other name, or a failed construction, returns
+ * DLM_ERR_NOT_FOUND with *handle = NULL.  The "sdxl" backend here takes its
+ * conditioning from the embeddings file (cond tensors as above, optional
+ * uncond_encoder_hidden_states_f16 / uncond_text_embeds_f16, zero when
+ * absent) instead of the reference's CLIP text encoders; generate() does not
+ * read the prompt strings, defaults steps <= 0 to 20 and cfg <= 0 to 7.5, and
+ * returns the native resolution (8 * latent_size). */
+typedef struct dlm_backend_config {
+  const char* backend_name;
+  const char* preset;
+  const char* unet_weights;
+  const char* vae_weights;
+  const char* embeds;
+  float vae_scaling_factor;
+  const dlm_unet_config* unet_cfg; /* NULL = SDXL */
+  const dlm_vae_config* vae_cfg;   /* NULL = SDXL */
+  int latent_size;                 /* <= 0: 128 */
+} dlm_backend_config;
+int dlm_backend_create(const dlm_backend_config* cfg, void** handle);
+int dlm_backend_destroy(void* handle);
+int dlm_backend_generate(void* handle, const char* prompt, const char* negative, int steps,
+                         uint64_t seed, float cfg, int w, int h, uint8_t* rgb_out,
+                         size_t rgb_capacity, int* w_out, int* h_out);
+int dlm_backend_info(void* handle, char* name, int name_len, int* latent_channels,
+                     int* native_resolution, int* needs_t5);
+/* "sdxl-1.0" or "sdxl-1.0/<preset>" (reference compose_model_id). */
+int dlm_backend_model_id(void* handle, char* buf, int len);
+/* LoRA names resolve to $DOLLAMA_LORA_DIR (default models/loras)/<name>.safetensors;
+ * names hold [A-Za-z0-9_.-] and do not start with '.'. */
+int dlm_backend_apply_loras(void* handle, const char* const* names, const float* strengths, int n);
+int dlm_backend_clear_loras(void* handle);
+
+/* Host only: out[k] = float(z_k * sigma0), z the reference's seeded normal
+ * stream (xorshift128+ seeded by splitmix64, Box-Muller;
+ * src/infer/diffusion.cu:80-136, :828-835). */
+int dlm_randn_latent(uint64_t seed, double sigma0, float* out, size_t n);
+
 /* VRAM arena statistics (src/kernels/device_arena.cuh DeviceArenaStats):
  * out[0..10] = cuda_malloc_calls, cuda_free_calls, chunk_alloc_calls,
  * alloc_calls, total_capacity, live_chunks, bytes_in_use, peak_bytes_in_use,

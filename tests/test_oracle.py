@@ -423,3 +423,90 @@ def test_rgb8_fixed_points():
     assert q.shape == (1, 1, 2, 3)
     # channel planes [-1, 1], [0, -3], [3, 0.5] -> pixels (-1, 0, 3) and (1, -3, 0.5)
     assert q[0, 0, 0].tolist() == [0, 128, 255] and q[0, 0, 1].tolist() == [255, 0, 191]
+
+
+# ------------------------------------------------------------------ noise --
+def test_splitmix64_known_answer():
+    """First SplitMix64 output for state 0: 0xE220A8397B1DCDAF
+    (16294208416658607535), the published test value."""
+    from oracle import noise_ref as NR
+    assert NR.splitmix64(0) == 0xE220A8397B1DCDAF
+
+
+def _berlekamp_massey(bits):
+    """Shortest LFSR over GF(2): connection polynomial (bit i = x^i) and length."""
+    C, B, L, m = 1, 1, 0, 1
+    for i, s in enumerate(bits):
+        d = s
+        for j in range(1, L + 1):
+            d ^= ((C >> j) & 1) & bits[i - j]
+        if d == 0:
+            m += 1
+        elif 2 * L <= i:
+            C, B, L, m = C ^ (B << m), C, i + 1 - L, 1
+        else:
+            C ^= B << m
+            m += 1
+    return C, L
+
+
+def _pmulmod(a, b, p, deg):
+    r = 0
+    while b:
+        if b & 1:
+            r ^= a
+        b >>= 1
+        a <<= 1
+        if (a >> deg) & 1:
+            a ^= p
+    return r
+
+
+def _ppow_x(e, p, deg):
+    r, base = 1, 2
+    while e:
+        if e & 1:
+            r = _pmulmod(r, base, p, deg)
+        base = _pmulmod(base, base, p, deg)
+        e >>= 1
+    return r
+
+
+def test_xorshift128plus_transition_is_full_period():
+    """The low output bit of xorshift128+ is a linear function of the state,
+    so its minimal polynomial is the transition's characteristic polynomial.
+    With the published shifts (23, 17, 26) that polynomial has degree 128 and
+    is primitive (period 2^128 - 1); a mistyped shift or operand breaks this."""
+    from oracle import noise_ref as NR
+    g = NR.XorShift128Plus(NR.splitmix64(7), NR.splitmix64(8))
+    bits = [g.step() & 1 for _ in range(600)]
+    C, L = _berlekamp_massey(bits)
+    assert L == 128
+    P = 0
+    for i in range(129):  # reciprocal polynomial x^128 C(1/x)
+        if (C >> i) & 1:
+            P |= 1 << (128 - i)
+    primes = [3, 5, 17, 257, 641, 65537, 274177, 6700417, 67280421310721]
+    order = (1 << 128) - 1
+    assert math.prod(primes) == order
+    assert _ppow_x(order, P, 128) == 1
+    for q in primes:
+        assert _ppow_x(order // q, P, 128) != 1
+
+
+def test_box_muller_pairing_and_moments():
+    """next() returns r cos(2 pi u2), then r sin(2 pi u2) with r^2 = -2 ln u1,
+    u1, u2 the generator's consecutive uniforms; N(0, 1) moments."""
+    from oracle import noise_ref as NR
+    a, b = NR.Randn(123), NR.Randn(123)
+    for _ in range(50):
+        u1 = b.uniform()
+        while u1 <= 1e-12:
+            u1 = b.uniform()
+        u2 = b.uniform()
+        z0, z1 = a.next(), a.next()
+        assert abs(z0 * z0 + z1 * z1 + 2.0 * math.log(u1)) < 1e-9
+        assert abs(math.atan2(z1, z0) % (2 * math.pi) - 2 * math.pi * u2) < 1e-9
+    z = NR.randn_latent(5, 1.0, 200000).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    assert abs((z ** 4).mean() - 3.0) < 0.05
