@@ -35,9 +35,11 @@ static GnPlan gn_plan(int N, int C, int HW) {
   while (p.S * p.R > 1024 && p.R > 1) --p.R;
   p.threads = p.S * p.R;
   // chunking depends on HW only, so each sample's statistics are computed
-  // identically whatever the batch size (B=2 == 2 x B=1, bit for bit)
+  // identically whatever the batch size (B=2 == 2 x B=1, bit for bit).
+  // About 1024 chunks per sample: a streaming pass needs several waves per
+  // CU in flight (256 chunks measured 3.4 TB/s on 1024x1024x128 fp32).
   (void)N;
-  const int target = 256;
+  const int target = 1024;
   p.chunk = std::max(p.R * 4, (HW + target - 1) / target);
   p.chunks = (HW + p.chunk - 1) / p.chunk;
   return p;
@@ -91,7 +93,22 @@ __global__ void gn_partial_kernel(const T* __restrict__ a, int Ca, int lda,
   load8(src + (size_t)p0 * ld, shift);
 #pragma unroll
   for (int i = 0; i < 8; ++i) s1[i] = s2[i] = 0.0f;
-  for (int p = p0 + r; p < p1; p += R) {
+  int p = p0 + r;
+  // four rows per iteration: four independent loads in flight per thread
+  for (; p + 3 * R < p1; p += 4 * R) {
+    float v[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load8(src + (size_t)(p + u * R) * ld, v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float d = v[u][i] - shift[i];
+        s1[i] += d;
+        s2[i] += d * d;
+      }
+  }
+  for (; p < p1; p += R) {
     float v[8];
     load8(src + (size_t)p * ld, v);
 #pragma unroll
