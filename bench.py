@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--loop-steps", type=int, default=20, help="Euler loop length (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-runs", type=int, default=3)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager forwards only (default: HIP-graph replay, eager timed beside it)")
     ap.add_argument("--workload", choices=("unet", "vae"), default="unet",
                     help="unet: the UNet step (default); vae: the VAE decode of one 1024x1024 image")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -152,19 +154,33 @@ def main():
     out = torch.empty(B, 4, H, W, dtype=torch.float16, device=dev)
     setup_s = time.time() - t_setup
 
-    for _ in range(args.warmup):
-        net.forward(latent, ts, ehs, text, ids, out=out)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    w0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        net.forward(latent, ts, ehs, text, ids, out=out)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - w0) / args.steps * 1e3
-    ms = e0.elapsed_time(e1) / args.steps
+    # all work on one created stream (HIP graphs cannot capture the null stream)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+
+    def timed(graphs):
+        net.set_graphs(graphs)
+        for _ in range(max(args.warmup, 3 if graphs else 0)):  # graphs: eager, capture, replay
+            net.forward(latent, ts, ehs, text, ids, out=out)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(args.steps):
+            net.forward(latent, ts, ehs, text, ids, out=out)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps, (time.perf_counter() - w0) / args.steps * 1e3
+
+    eager_ms, eager_wall = timed(False)
+    eager_out = out.clone()
+    if args.eager:
+        ms, wall = eager_ms, eager_wall
+    else:
+        ms, wall = timed(True)
+        if not torch.equal(out, eager_out):
+            raise RuntimeError("graph replay differs from the eager forward")
+        net.set_graphs(False)
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite noise_pred")
 
@@ -197,6 +213,7 @@ def main():
     if args.loop_steps > 0:
         sig, _ = U.euler_schedule(args.loop_steps)
         lat32 = torch.randn(4, H, W, generator=g, device=dev) * sig[0]
+        net.set_graphs(not args.eager)
         lt = lat32.clone()
         U.denoise(net, lt, ehs, text, ids, steps=args.loop_steps, guidance=7.5)  # warm
         lt = lat32.clone()
@@ -205,7 +222,8 @@ def main():
         U.denoise(net, lt, ehs, text, ids, steps=args.loop_steps, guidance=7.5)
         torch.cuda.synchronize()
         loop = {"steps": args.loop_steps, "guidance": 7.5, "s": round(time.perf_counter() - l0, 4),
-                "finite": bool(torch.isfinite(lt).all())}
+                "finite": bool(torch.isfinite(lt).all()), "graphs": not args.eager}
+        net.set_graphs(False)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.seed)
 
@@ -225,6 +243,8 @@ def main():
         "config": {"workload": "sdxl_unet_step_1024px_cfg_b2", "batch": B, "latent": [4, H, W],
                    "ctx": [L, cfg.cross_dim], "params": 2567463684},
         "wall_ms_per_step": round(wall, 3),
+        "timing": "eager forwards" if args.eager else "HIP-graph replay of the forward (one hipGraphLaunch per step)",
+        "eager_ms_per_step": round(eager_ms, 3),
         "step_tflop": round(fl["total"] / 1e12, 4),
         "whole_step_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 1),
         "whole_step_frac_mfma": round(fl["total"] / (ms * 1e-3) / MFMA_FP16_PEAK, 4),

@@ -253,6 +253,20 @@ int dlm_unet_set_stage_hook(void* handle, dlm_unet_stage_hook hook, void* user) 
   });
 }
 
+int dlm_unet_set_graphs(void* handle, int on) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<UNet*>(handle)->set_graphs(on != 0);
+  });
+}
+
+int dlm_unet_graphs_captured(void* handle, size_t* count) {
+  return guarded([&] {
+    if (!handle || !count) throw std::invalid_argument("NULL argument");
+    *count = static_cast<UNet*>(handle)->graphs_captured();
+  });
+}
+
 int dlm_unet_set_profiling(void* handle, int on) {
   return guarded([&] {
     if (!handle) throw std::invalid_argument("NULL handle");

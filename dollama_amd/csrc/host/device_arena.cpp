@@ -34,6 +34,7 @@ struct Arena {
   // pool-off mode: every allocation is a separate block, freed on rewind
   std::vector<void*> direct;
   DeviceArenaStats st;
+  uint64_t epoch = 0;  // bumped whenever the chunk list changes
 };
 
 Arena g_arenas[kDeviceArenaCount];
@@ -142,11 +143,20 @@ void* device_arena_alloc(DeviceArenaId id, size_t bytes) {
     a.st.cuda_malloc_calls++;
     a.st.chunk_alloc_calls++;
     a.chunks.push_back(c);
+    a.epoch++;
     a.st.total_capacity += c.bytes;
     a.st.live_chunks = a.chunks.size();
     a.cur_chunk = a.chunks.size() - 1;
     a.cur_off = 0;
   }
+}
+
+uint64_t device_arena_epoch(DeviceArenaId id) {
+  Arena& a = arena(id);
+  std::lock_guard<std::mutex> lock(a.mu);
+  // pool-off mode hands out fresh blocks on every allocation: no two calls
+  // see the same addresses, so every call is a new epoch
+  return device_arena_pool_enabled() ? a.epoch : ++a.epoch;
 }
 
 void device_arena_rewind(const DeviceArenaMark& m) {
@@ -182,6 +192,7 @@ void device_arena_reserve(DeviceArenaId id, size_t bytes) {
     a.st.cuda_free_calls++;
   }
   a.chunks.clear();
+  a.epoch++;
   a.st.total_capacity = 0;
   Chunk c;
   c.bytes = std::max(align_up(bytes), kDeviceArenaAlign);
@@ -206,6 +217,7 @@ void device_arena_release(DeviceArenaId id) {
     a.st.cuda_free_calls++;
   }
   a.chunks.clear();
+  a.epoch++;
   a.cur_chunk = 0;
   a.cur_off = 0;
   a.st.total_capacity = 0;

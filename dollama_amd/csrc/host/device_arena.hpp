@@ -59,6 +59,10 @@ bool device_arena_release_noexcept(DeviceArenaId id) noexcept;
 DeviceArenaStats device_arena_stats(DeviceArenaId id);
 void device_arena_reset_counters(DeviceArenaId id);
 size_t device_arena_first_chunk_bytes(DeviceArenaId id);
+// Changes whenever the arena's chunk list changes (new chunk, reserve,
+// release): equal epoch and equal mark mean that the same sequence of
+// allocations returns the same addresses (used to reuse captured graphs).
+uint64_t device_arena_epoch(DeviceArenaId id);
 
 class DeviceArenaScope {
  public:

@@ -84,11 +84,14 @@ void denoise(UNet& unet, const DenoiseArgs& a, void* stream, bool cfg) {
   DLM_CALL(dlm_memcpy(d_t, host_t.data(), host_t.size() * sizeof(float), 0));
   void* model_in = scope.alloc<uint16_t>((size_t)B * n);
   void* noise = scope.alloc<uint16_t>((size_t)B * n);
+  // the step's timesteps are copied into one slot, so every forward of the
+  // loop has the same arguments (one captured graph serves all steps)
+  float* d_tslot = scope.alloc<float>(B);
 
   DLM_CALL(dlm_scale_latent_fp16(a.latent, model_in, n, (float)sched.input_scale(0), B, stream));
   for (int i = 0; i < a.steps; ++i) {
-    unet.forward(B, a.H, a.W, model_in, d_t + (size_t)B * i, a.ehs, a.ctx_len, a.text, a.time_ids, 0,
-                 noise, stream);
+    DLM_CALL(dlm_memcpy_async(d_tslot, d_t + (size_t)B * i, B * sizeof(float), 2, stream));
+    unet.forward(B, a.H, a.W, model_in, d_tslot, a.ehs, a.ctx_len, a.text, a.time_ids, 0, noise, stream);
     const float next_scale = i + 1 < a.steps ? (float)sched.input_scale(i + 1) : 1.0f;
     if (cfg)
       DLM_CALL(dlm_euler_cfg_step(a.latent, noise, model_in, n, a.guidance, sg[i], sg[i + 1], next_scale,

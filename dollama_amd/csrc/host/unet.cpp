@@ -155,6 +155,7 @@ UNet::UNet(const UNetConfig& cfg) : cfg_(cfg) {
 }
 
 UNet::~UNet() {
+  clear_graphs();
   for (Backup& b : backups_) (void)dlm_free(b.copy);
   if (packed_) (void)dlm_free(packed_);
   for (void* e : prof_events_) (void)dlm_event_destroy(e);
@@ -562,7 +563,19 @@ void UNet::pack_all(void* stream) {
   }
 }
 
+void UNet::set_graphs(bool on) {
+  graphs_on_ = on;
+  if (!on) clear_graphs();
+}
+
+void UNet::clear_graphs() {
+  for (auto& kv : graphs_) (void)dlm_graph_destroy(kv.second);
+  graphs_.clear();
+  seen_.clear();
+}
+
 void UNet::prepare(void* stream) {
+  clear_graphs();  // captured graphs hold the old packed weight addresses
   // a re-pack starts from the registered weights: earlier LoRA state is void
   for (Backup& b : backups_) (void)dlm_free(b.copy);
   backups_.clear();
@@ -814,6 +827,55 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
 void UNet::forward(int B, int H, int W, const void* latent, const float* d_timesteps,
                    const void* ehs, int ctx_len, const void* text, const void* time_ids,
                    int ids_bstride, void* out, void* stream) {
+  if (!graphs_on_ || hook_ || prof_on_ || !stream || !packed_) {
+    forward_impl(B, H, W, latent, d_timesteps, ehs, ctx_len, text, time_ids, ids_bstride, out, stream);
+    return;
+  }
+  auto words = [](const void* p) { return (uint64_t)(uintptr_t)p; };
+  const DeviceArenaMark m0 = device_arena_mark(DeviceArenaId::UNet);
+  const DeviceArenaMark m1 = device_arena_mark(DeviceArenaId::UNetPersist);
+  const uint64_t e0 = device_arena_epoch(DeviceArenaId::UNet);
+  const uint64_t e1 = device_arena_epoch(DeviceArenaId::UNetPersist);
+  const std::vector<uint64_t> key = {
+      (uint64_t)B, (uint64_t)H, (uint64_t)W, (uint64_t)ctx_len, (uint64_t)ids_bstride, words(latent),
+      words(d_timesteps), words(ehs), words(text), words(time_ids), words(out), words(stream),
+      m0.chunk, m0.offset, m1.chunk, m1.offset, e0, e1};
+  auto it = graphs_.find(key);
+  if (it != graphs_.end()) {
+    DLM_CALL(dlm_graph_launch(it->second, stream));
+    return;
+  }
+  if (!seen_.count(key)) {  // first sight: run eagerly (allocates chunks and workspaces)
+    if (seen_.size() >= 64) clear_graphs();
+    seen_.insert(key);
+    forward_impl(B, H, W, latent, d_timesteps, ehs, ctx_len, text, time_ids, ids_bstride, out, stream);
+    return;
+  }
+  DLM_CALL(dlm_graph_begin_capture(stream));
+  void* exec = nullptr;
+  try {
+    forward_impl(B, H, W, latent, d_timesteps, ehs, ctx_len, text, time_ids, ids_bstride, out, stream);
+  } catch (...) {
+    void* junk = nullptr;
+    (void)dlm_graph_end_capture(stream, &junk);
+    (void)dlm_graph_destroy(junk);
+    throw;
+  }
+  DLM_CALL(dlm_graph_end_capture(stream, &exec));
+  if (device_arena_epoch(DeviceArenaId::UNet) != e0 ||
+      device_arena_epoch(DeviceArenaId::UNetPersist) != e1) {
+    // an arena grew during the capture: do not keep the graph, run eagerly
+    (void)dlm_graph_destroy(exec);
+    forward_impl(B, H, W, latent, d_timesteps, ehs, ctx_len, text, time_ids, ids_bstride, out, stream);
+    return;
+  }
+  graphs_[key] = exec;
+  DLM_CALL(dlm_graph_launch(exec, stream));
+}
+
+void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_timesteps,
+                        const void* ehs, int ctx_len, const void* text, const void* time_ids,
+                        int ids_bstride, void* out, void* stream) {
   if (!packed_) throw std::runtime_error("UNet::forward: prepare() has not run");
   if (B <= 0 || B > 16) throw std::invalid_argument("UNet::forward: B must be in [1, 16]");
   if (H % 4 != 0 || W % 4 != 0 || H < 8 || W < 8)

@@ -22,6 +22,8 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
+#include <set>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -96,6 +98,17 @@ class UNet {
     hook_user_ = user;
   }
 
+  // HIP-graph replay of forward().  With graphs on, a forward whose
+  // arguments, stream and arena state (mark and chunk epoch of the UNet and
+  // UNetPersist arenas) equal those of an earlier forward replays that
+  // forward's captured graph.  The first such forward runs eagerly (it
+  // allocates every arena chunk and split-K workspace), the second is
+  // captured and launched, later ones launch the graph.  Needs a created
+  // stream (not the null stream); inactive while a stage hook or profiling
+  // is on.  Replays are stream-ordered like the eager forward they replace.
+  void set_graphs(bool on);
+  size_t graphs_captured() const { return graphs_.size(); }
+
   // Per-launch timing with device events, grouped by kernel class.  While
   // enabled, every launch of a forward is bracketed by two events; the
   // report (after the stream is synchronised) gives per class the launch
@@ -164,6 +177,14 @@ class UNet {
   T2D pack_t2d(const std::string& p, int C, int depth, void* stream);
   Conv pack_conv(const std::string& p, int Co, int Ci, int k, int cin_pad, void* stream);
   void pack_all(void* stream);
+
+  void forward_impl(int B, int H, int W, const void* latent, const float* d_timesteps,
+                    const void* ehs, int ctx_len, const void* text, const void* time_ids,
+                    int ids_bstride, void* out, void* stream);
+  void clear_graphs();
+  bool graphs_on_ = false;
+  std::map<std::vector<uint64_t>, void*> graphs_;
+  std::set<std::vector<uint64_t>> seen_;
 
   // forward pieces
   void resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out, int B,

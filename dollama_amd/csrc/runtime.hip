@@ -193,6 +193,38 @@ int dlm_stream_synchronize(void* stream) {
   return DLM_OK;
 }
 
+int dlm_graph_begin_capture(void* stream) {
+  DLM_REQUIRE(stream != nullptr, "graph capture needs a created stream (not the null stream)");
+  DLM_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+  return DLM_OK;
+}
+
+int dlm_graph_end_capture(void* stream, void** exec) {
+  DLM_REQUIRE(stream && exec, "NULL argument");
+  *exec = nullptr;
+  hipGraph_t g = nullptr;
+  DLM_HIP(hipStreamEndCapture((hipStream_t)stream, &g));
+  if (!g) return dlm::fail(DLM_ERR_HIP, "graph capture produced no graph");
+  hipGraphExec_t e = nullptr;
+  const hipError_t st = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (st != hipSuccess) return dlm::fail(DLM_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(st));
+  *exec = (void*)e;
+  return DLM_OK;
+}
+
+int dlm_graph_launch(void* exec, void* stream) {
+  DLM_REQUIRE(exec != nullptr, "exec is NULL");
+  DLM_HIP(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream));
+  return DLM_OK;
+}
+
+int dlm_graph_destroy(void* exec) {
+  if (exec == nullptr) return DLM_OK;
+  DLM_HIP(hipGraphExecDestroy((hipGraphExec_t)exec));
+  return DLM_OK;
+}
+
 int dlm_event_create(void** event) {
   DLM_REQUIRE(event != nullptr, "event is NULL");
   hipEvent_t e = nullptr;

@@ -62,6 +62,8 @@ HOST_SIGNATURES = {
     "dlm_unet_forward": (I, [P, I, I, I, P, P, P, I, P, P, I, P, P]),
     "dlm_unet_set_stage_hook": (I, [P, STAGE_HOOK, P]),
     "dlm_unet_set_profiling": (I, [P, I]),
+    "dlm_unet_set_graphs": (I, [P, I]),
+    "dlm_unet_graphs_captured": (I, [P, POINTER(c_size_t)]),
     "dlm_unet_profile_report": (I, [P, POINTER(ctypes.c_double), P]),
     "dlm_euler_schedule": (I, [I, POINTER(ctypes.c_float), POINTER(ctypes.c_float)]),
     "dlm_pipeline_denoise": (I, [P, I, ctypes.c_float, I, I, P, P, I, P, P, P]),
@@ -275,6 +277,16 @@ class UNet:
         _call("dlm_unet_read_weight", self._h, name.encode(), c_void_p(out.data_ptr()),
               out.numel() * 2, _stream())
         return out
+
+    def set_graphs(self, on: bool):
+        """HIP-graph replay of repeated forwards (needs a non-default torch stream)."""
+        _call("dlm_unet_set_graphs", self._h, int(bool(on)))
+
+    @property
+    def graphs_captured(self) -> int:
+        v = c_size_t()
+        _call("dlm_unet_graphs_captured", self._h, ctypes.byref(v))
+        return v.value
 
     KERNEL_CLASSES = ("conv", "linear", "attention", "groupnorm", "layernorm", "other")
 

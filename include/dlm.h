@@ -71,6 +71,15 @@ int dlm_mem_get_info(size_t* free_bytes, size_t* total_bytes);
 int dlm_stream_create(void** stream);
 int dlm_stream_destroy(void* stream);
 int dlm_stream_synchronize(void* stream);
+/* HIP graphs: capture the work enqueued on a created stream (thread-local
+ * capture mode), instantiate it, replay it.  end_capture returns the
+ * executable graph; the captured work itself does not run until launched.
+ * Replaces the reference's CUDA-graph switch (FastConfig::graphs,
+ * src/server/fast_config.hpp). */
+int dlm_graph_begin_capture(void* stream);
+int dlm_graph_end_capture(void* stream, void** exec);
+int dlm_graph_launch(void* exec, void* stream);
+int dlm_graph_destroy(void* exec);
 int dlm_event_create(void** event);
 int dlm_event_destroy(void* event);
 int dlm_event_record(void* event, void* stream);

@@ -106,6 +106,18 @@ typedef void (*dlm_unet_stage_hook)(const char* name, const void* dptr, size_t n
                                     void* user);
 int dlm_unet_set_stage_hook(void* handle, dlm_unet_stage_hook hook, void* user);
 
+/* HIP-graph replay of the forward (the reference's CUDA-graph mode,
+ * FastConfig::graphs).  With graphs on, a forward on a created stream whose
+ * arguments and arena state equal an earlier forward's replays that
+ * forward's captured graph: the first such call runs eagerly, the second is
+ * captured and launched, later ones launch (about 850 kernels per SDXL
+ * step in one hipGraphLaunch).  Results equal the eager forward's bit for
+ * bit.  Inactive on the null stream, with a stage hook or with profiling;
+ * dlm_unet_prepare drops the captured graphs.  The denoise loop passes the
+ * same arguments every step, so one graph serves the whole loop. */
+int dlm_unet_set_graphs(void* handle, int on);
+int dlm_unet_graphs_captured(void* handle, size_t* count);
+
 /* Per-launch kernel timing (device events around every launch of a
  * forward).  Classes: 0 conv, 1 linear, 2 attention, 3 groupnorm,
  * 4 layernorm, 5 other.  report fills, per class, out[4*c + 0..3] =
