@@ -569,6 +569,62 @@ int dlm_randn_latent(uint64_t seed, double sigma0, float* out, size_t n) {
   });
 }
 
+// ------------------------------------------------------------------ safetensors
+
+int dlm_st_open(const char* path, void** handle) {
+  return guarded([&] {
+    if (!path || !handle) throw std::invalid_argument("NULL argument");
+    *handle = nullptr;
+    *handle = new SafeTensors(path);
+  });
+}
+
+int dlm_st_close(void* handle) {
+  return guarded([&] { delete static_cast<SafeTensors*>(handle); });
+}
+
+int dlm_st_count(void* handle, int* count) {
+  return guarded([&] {
+    if (!handle || !count) throw std::invalid_argument("NULL argument");
+    *count = (int)static_cast<SafeTensors*>(handle)->names().size();
+  });
+}
+
+int dlm_st_name(void* handle, int index, char* buf, int len) {
+  return guarded([&] {
+    if (!handle || !buf || len <= 0) throw std::invalid_argument("NULL argument");
+    const auto& ns = static_cast<SafeTensors*>(handle)->names();
+    if (index < 0 || index >= (int)ns.size()) throw std::invalid_argument("index out of range");
+    if ((int)ns[index].size() >= len) throw std::invalid_argument("buffer too small");
+    std::memcpy(buf, ns[index].c_str(), ns[index].size() + 1);
+  });
+}
+
+int dlm_st_info(void* handle, const char* name, int* dtype, int* ndim, int64_t* shape, size_t* nbytes) {
+  return guarded([&] {
+    if (!handle || !name || !dtype || !ndim || !shape || !nbytes) throw std::invalid_argument("NULL argument");
+    const SafeTensors& st = *static_cast<SafeTensors*>(handle);
+    if (!st.has(name)) throw std::out_of_range(std::string("safetensors: no tensor '") + name + "'");
+    *dtype = (int)st.dtype(name);
+    const auto& sh = st.shape(name);
+    if (sh.size() > 8) throw std::invalid_argument("more than 8 dimensions");
+    *ndim = (int)sh.size();
+    for (size_t i = 0; i < sh.size(); ++i) shape[i] = sh[i];
+    st.tensor_bytes(name, *nbytes);
+  });
+}
+
+int dlm_st_read(void* handle, const char* name, void* out, size_t bytes) {
+  return guarded([&] {
+    if (!handle || !name || (!out && bytes)) throw std::invalid_argument("NULL argument");
+    const SafeTensors& st = *static_cast<SafeTensors*>(handle);
+    size_t nb = 0;
+    const uint8_t* p = st.tensor_bytes(name, nb);
+    if (bytes != nb) throw std::invalid_argument("byte count mismatch");
+    std::memcpy(out, p, nb);
+  });
+}
+
 int dlm_arena_stats(int id, uint64_t* out) {
   return guarded([&] {
     if (!out) throw std::invalid_argument("NULL out");

@@ -264,6 +264,24 @@ int dlm_backend_clear_loras(void* handle);
  * src/infer/diffusion.cu:80-136, :828-835). */
 int dlm_randn_latent(uint64_t seed, double sigma0, float* out, size_t n);
 
+/* ------------------------------------------------------------------ */
+/* safetensors reader (host)                                           */
+/* ------------------------------------------------------------------ */
+
+/* Memory-mapped read-only safetensors file (reference SafeTensors,
+ * src/io/safetensors.hpp:108: names / dtype / shape / tensor_bytes).  A
+ * missing file, a header length beyond the file or malformed JSON fails at
+ * open; an unknown name is DLM_ERR_NOT_FOUND.  dtype codes: 0 F64, 1 F32,
+ * 2 F16, 3 BF16, 4 I64, 5 I32, 6 I16, 7 I8, 8 U8, 9 BOOL, 10 other.
+ * __metadata__ is not a tensor. */
+int dlm_st_open(const char* path, void** handle);
+int dlm_st_close(void* handle);
+int dlm_st_count(void* handle, int* count);
+int dlm_st_name(void* handle, int index, char* buf, int len);
+int dlm_st_info(void* handle, const char* name, int* dtype, int* ndim, int64_t* shape /* [8] */,
+                size_t* nbytes);
+int dlm_st_read(void* handle, const char* name, void* out, size_t bytes);
+
 /* VRAM arena statistics (src/kernels/device_arena.cuh DeviceArenaStats):
  * out[0..10] = cuda_malloc_calls, cuda_free_calls, chunk_alloc_calls,
  * alloc_calls, total_capacity, live_chunks, bytes_in_use, peak_bytes_in_use,
