@@ -284,21 +284,25 @@ __device__ __forceinline__ void epilogue_tile(const f32x16& a, int row0, int col
   }
 }
 
-// GEGLU epilogue of a (value, gate) pair of 32x32 blocks: the packed weight
-// puts value rows 32p..32p+31 and the matching gate rows in adjacent 32-row
-// blocks, so both halves of an output element sit in the same lane and
-// register.  `ocol` is the output column of this lane.
-__device__ __forceinline__ void epilogue_geglu_tile(const f32x16& av, const f32x16& ag, int row0,
-                                                    int col, int ocol, int lane,
+// GEGLU epilogue of one 32x32 accumulator block.  The packed weight
+// interleaves value and gate rows in groups of 4 (see geglu_pack_kernel), so
+// packed column c is a value when (c & 4) == 0 and its gate is column c ^ 4,
+// held by lane ^ 4 in this layout (lane owns column `col`).  Every lane takes
+// part in the exchange; value lanes write output column (c / 8) * 4 + c % 4.
+__device__ __forceinline__ void epilogue_geglu_tile(const f32x16& a, int row0, int col, int lane,
                                                     const EpiArgs& ep) {
-  if (col >= ep.N) return;
+  float partner[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) partner[e] = __shfl_xor(a[e], 4, 64);
+  if ((col & 4) || col >= ep.N) return;
+  const int ocol = (col >> 3) * 4 + (col & 3);
   const float bv = ep.bias ? (float)ep.bias[col] : 0.0f;
-  const float bg = ep.bias ? (float)ep.bias[col + 32] : 0.0f;
+  const float bg = ep.bias ? (float)ep.bias[col + 4] : 0.0f;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int row = row0 + mfma_row(e, lane);
     if (row < ep.M) {
-      float v = (av[e] * ep.alpha + bv) * gelu_erf_f(ag[e] * ep.alpha + bg);
+      float v = (a[e] * ep.alpha + bv) * gelu_erf_f(partner[e] * ep.alpha + bg);
       if (ep.res) v += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol];
       ep.y[(size_t)row * ep.ldy + ocol] = (f16)v;
     }
@@ -475,18 +479,13 @@ mfma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n) {
 
   // ------------------------------ epilogue ------------------------------
   const int row_base = m0 + wm * WM;
-  if constexpr (TN % 2 == 0) {
-    if (ep.act == DLM_ACT_GEGLU) {
+  if (ep.act == DLM_ACT_GEGLU) {
 #pragma unroll
-      for (int j = 0; j < TN; j += 2)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int col = n0 + wn * WN + j * 32 + (lane & 31);
-          const int ocol = (n0 + wn * WN) / 2 + (j / 2) * 32 + (lane & 31);
-          epilogue_geglu_tile(acc[i][j], acc[i][j + 1], row_base + i * 32, col, ocol, lane, ep);
-        }
-      return;
-    }
+      for (int i = 0; i < TM; ++i)
+        epilogue_geglu_tile(acc[i][j], row_base + i * 32, n0 + wn * WN + j * 32 + (lane & 31), lane, ep);
+    return;
   }
 #pragma unroll
   for (int j = 0; j < TN; ++j)
@@ -761,34 +760,41 @@ __device__ __forceinline__ void epi4(const f32x4& a, int row, int col, const Epi
   }
 }
 
-// GEGLU epilogue: value block av and gate block ag of the same 32 output
-// columns; col is the packed value column, ocol the output column.
-__device__ __forceinline__ void epi4_geglu(const f32x4& av, const f32x4& ag, int row, int col,
-                                           int ocol, const EpiArgs& ep) {
-  if (row >= ep.M || col >= ep.N) return;
-  float v[4], g[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    v[t] = av[t] * ep.alpha;
-    g[t] = ag[t] * ep.alpha;
-  }
+// GEGLU epilogue of one 16x16 block.  Value and gate rows of the packed
+// weight alternate in groups of 4 (geglu_pack_kernel), so the lane's 4
+// packed columns col..col+3 are values when (col & 4) == 0 and the matching
+// gates are held by lane ^ 16.  The pair splits the group: the value lane
+// computes output columns 0-1 of the group, the gate lane columns 2-3, each
+// after one exchange of two values (no lane idles).
+__device__ __forceinline__ void epi4_geglu(const f32x4& a, int row, int col, const EpiArgs& ep) {
+  const bool is_gate = (col & 4) != 0;
+  // value lane sends values 2-3, gate lane sends gates 0-1
+  const float r0 = __shfl_xor(is_gate ? a[0] : a[2], 16, 64);
+  const float r1 = __shfl_xor(is_gate ? a[1] : a[3], 16, 64);
+  const int vcol = col & ~4;            // packed column of value 0 of the group
+  const int t0 = is_gate ? 2 : 0;       // group columns this lane computes
+  if (row >= ep.M || vcol >= ep.N) return;
+  float v[2], g[2];
+  v[0] = (is_gate ? r0 : a[0]) * ep.alpha;
+  v[1] = (is_gate ? r1 : a[1]) * ep.alpha;
+  g[0] = (is_gate ? a[2] : r0) * ep.alpha;
+  g[1] = (is_gate ? a[3] : r1) * ep.alpha;
   if (ep.bias) {
-    const f16x4 bv = ld4h(ep.bias + col), bg = ld4h(ep.bias + col + 32);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      v[t] += (float)bv[t];
-      g[t] += (float)bg[t];
+    for (int t = 0; t < 2; ++t) {
+      v[t] += (float)ep.bias[vcol + t0 + t];
+      g[t] += (float)ep.bias[vcol + 4 + t0 + t];
     }
   }
 #pragma unroll
-  for (int t = 0; t < 4; ++t) v[t] *= gelu_erf_fast(g[t]);  // A&S erf: -0.25 ms per UNet step
+  for (int t = 0; t < 2; ++t) v[t] *= gelu_erf_fast(g[t]);  // A&S erf: -0.25 ms per UNet step
+  const int ocol = (vcol >> 1) + t0;
   if (ep.res) {
-    const f16x4 r = ld4h(ep.res + (size_t)row * ep.ldr + ocol);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)r[t];
+    for (int t = 0; t < 2; ++t) v[t] += ep.beta * (float)ep.res[(size_t)row * ep.ldr + ocol + t];
   }
-  const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-  *reinterpret_cast<f16x4*>(ep.y + (size_t)row * ep.ldy + ocol) = o;
+  f16 o2[2] = {(f16)v[0], (f16)v[1]};
+  *reinterpret_cast<uint32_t*>(ep.y + (size_t)row * ep.ldy + ocol) = *reinterpret_cast<uint32_t*>(o2);
 }
 
 // Split-K: the K slices of a tile are divided into S ranges of kps slices,
@@ -1013,20 +1019,12 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   // block i and output columns 4 (lane >> 4) + [0, 4) of block j.
   const int row0 = m0 + wm * WM + (lane & 15);
   const int col0 = n0 + wn * WN + 4 * (lane >> 4);
-  if constexpr (TN % 4 == 0) {
-    if (ep.act == DLM_ACT_GEGLU) {
-      // 64-column groups: blocks 0,1 are values, blocks 2,3 their gates
-      const int ocol0 = (n0 + wn * WN) / 2 + 4 * (lane >> 4);
+  if (ep.act == DLM_ACT_GEGLU) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int g = 0; g < TN / 4; ++g)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            epi4_geglu(acc[i][4 * g + h], acc[i][4 * g + h + 2], row0 + i * 16,
-                       col0 + (4 * g + h) * 16, ocol0 + g * 32 + h * 16, ep);
-      return;
-    }
+      for (int j = 0; j < TN; ++j) epi4_geglu(acc[i][j], row0 + i * 16, col0 + j * 16, ep);
+    return;
   }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -1078,8 +1076,6 @@ template <int BM, int BN, int WM, int WN, int NS, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                       hipStream_t s, int S = 1) {
   static_assert(NS * (BM + BN) * BK * 2 <= 160 * 1024, "LDS ring larger than 160 KiB");
-  if (ep.act == DLM_ACT_GEGLU && WN % 64 != 0)
-    return fail(DLM_ERR_UNSUPPORTED, "GEGLU needs 64-column wave tiles");
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
@@ -1145,13 +1141,7 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
     return fail(DLM_ERR_UNSUPPORTED, "fp32 output/residual with a GEGLU or V^T epilogue");
   const bool dma = dma_epilogue_ok(ep) && dma_operand_ok(ad) && dma_operand_ok(bd);
   if (dma) {
-    // GEGLU pairs value/gate blocks inside one wave: only 64-column waves
-    switch (ep.act == DLM_ACT_GEGLU &&
-                    (g_forced_tile == 9 || g_forced_tile == 11 || g_forced_tile == 14 ||
-                     g_forced_tile == 15 || g_forced_tile == 18 || g_forced_tile == 20 ||
-                     (g_forced_tile >= 21 && g_forced_tile <= 26))
-                ? 0
-                : g_forced_tile) {
+    switch (g_forced_tile) {
       case 8: return launch_dma<128, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
       case 9: return launch_dma<128, 64, 64, 32, 2>(ad, bd, ep, M, N, s);
       case 10: return launch_dma<128, 128, 64, 64, 4>(ad, bd, ep, M, N, s);
@@ -1173,19 +1163,16 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
       case 26: return launch_dma<128, 80, 16, 80, 5>(ad, bd, ep, M, N, s);
       default: break;
     }
-    if (g_forced_tile == 0 || ep.act == DLM_ACT_GEGLU) {
+    if (g_forced_tile == 0) {
       // Measured on the UNet's shapes (warmed-up clocks, N(0,1) data):
-      // 8-wave tiles (two waves per SIMD) everywhere.  GEGLU needs 64-column
-      // waves (value and gate blocks in one wave): 256x128 tiles with a
-      // three-slice ring where they fill the chip (75 us vs 120 us for the
-      // 128x128 two-slice form on 2048x10240x1280).  128x128 tiles: two
+      // 8-wave tiles (two waves per SIMD) everywhere.  128x128 tiles: two
       // slices in flight when two workgroups share a CU, four when the grid
-      // leaves CUs with one.
+      // leaves CUs with one.  GEGLU takes the same tiles (its value/gate
+      // pairs sit in lanes 16 apart, so any 16-column-multiple wave works):
+      // 128x128 two-slice 71 / 81 us on 2048x10240x1280 / 8192x5120x640,
+      // against 77 / 90 us for the 256x128 three-slice tiles the earlier
+      // 64-column pairing needed.
       const long long t128 = ceil_div(M, 128) * ceil_div(N, 128);
-      if (ep.act == DLM_ACT_GEGLU)
-        return ceil_div(M, 256) * ceil_div(N, 128) >= kCUs
-                   ? launch_dma<256, 128, 64, 64, 3>(ad, bd, ep, M, N, s)
-                   : launch_dma<128, 128, 32, 64, 4>(ad, bd, ep, M, N, s);
       // Output widths that are multiples of 160 (SDXL's 320 / 640 / 1280
       // channels): 160-column tiles give whole waves of tiles on 256 CUs
       // where 128-column tiles leave a partial wave; few tiles with a long K
@@ -1363,13 +1350,16 @@ __global__ void conv_weight_pack_add_kernel(const f16* __restrict__ w, f16* __re
   }
 }
 
-// GEGLU interleave in 32-row block pairs: packed row 64p+s <- value row
-// 32p+s (s<32) or gate row d+32p+s-32 (s>=32).
+// GEGLU interleave in groups of 4: packed row 8q+s <- value row 4q+s (s<4)
+// or gate row d+4q+s-4 (s>=4).  A 16-column MFMA block then holds two
+// (value, gate) groups whose halves sit in lanes that differ by 16 (16x16
+// form) or 4 (32x32 form), so any tile width that is a multiple of 16 can
+// pair them.
 __global__ void geglu_pack_kernel(const f16* __restrict__ w, const f16* __restrict__ b,
                                   f16* __restrict__ wo, f16* __restrict__ bo, int d, int K) {
   const int r = blockIdx.x;  // packed row
-  const int q = r >> 6, s = r & 63;
-  const int src = s < 32 ? 32 * q + s : d + 32 * q + (s - 32);
+  const int q = r >> 3, s = r & 7;
+  const int src = s < 4 ? 4 * q + s : d + 4 * q + (s - 4);
   for (int k = threadIdx.x; k < K; k += blockDim.x) wo[(size_t)r * K + k] = w[(size_t)src * K + k];
   if (threadIdx.x == 0 && b && bo) bo[r] = b[src];
 }
@@ -1503,7 +1493,7 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
               "X or W larger than 2 GiB");
   DLM_REQUIRE(act >= DLM_ACT_NONE && act <= DLM_ACT_GELU, "unknown act");
   if (act == DLM_ACT_GEGLU) {
-    DLM_REQUIRE(N % 64 == 0, "GEGLU needs N (interleaved value+gate columns) % 64 == 0");
+    DLM_REQUIRE(N % 16 == 0, "GEGLU needs N (interleaved value+gate columns) % 16 == 0");
     DLM_REQUIRE(ldy >= N / 2, "ldy smaller than N/2");
     DLM_REQUIRE(!R || ldr >= N / 2, "ldr smaller than N/2");
   } else {
@@ -1612,7 +1602,7 @@ int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias
                         void* stream) {
   if (d <= 0 || K <= 0) return DLM_OK;
   DLM_REQUIRE(w && w_out, "NULL pointer");
-  DLM_REQUIRE(d % 32 == 0, "d must be a multiple of 32");
+  DLM_REQUIRE(d % 4 == 0, "d must be a multiple of 4");
   hipLaunchKernelGGL(geglu_pack_kernel, dim3(2 * d), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)w, (const f16*)bias, (f16*)w_out, (f16*)bias_out, d, K);
   DLM_LAUNCH_CHECK();

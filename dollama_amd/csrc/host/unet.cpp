@@ -228,11 +228,11 @@ void UNet::read_weight(const std::string& key, void* host, size_t bytes, void* s
   uint16_t* out = static_cast<uint16_t*>(host);
   if (pl.kind == Placement::kCopy) {
     std::copy(raw.begin(), raw.end(), out);
-  } else if (pl.kind == Placement::kGeglu) {  // packed row 64q+s <- value 32q+s | gate d+32q+s-32
+  } else if (pl.kind == Placement::kGeglu) {  // packed row 8q+s <- value 4q+s | gate d+4q+s-4
     const int d = pl.Co / 2, K = pl.Ci;
     for (int r = 0; r < pl.Co; ++r) {
-      const int q = r / 64, s = r % 64;
-      const int src = s < 32 ? 32 * q + s : d + 32 * q + (s - 32);
+      const int q = r / 8, s = r % 8;
+      const int src = s < 4 ? 4 * q + s : d + 4 * q + (s - 4);
       std::copy(raw.begin() + (size_t)r * K, raw.begin() + (size_t)(r + 1) * K, out + (size_t)src * K);
     }
   } else {  // packed [co][col0 + tap * cin_pad + ci] <- [co][ci][tap]
@@ -427,7 +427,7 @@ UNet::T2D UNet::pack_t2d(const std::string& p, int C, int depth, void* stream) {
     k.wq2 = copy_of(b + "attn2.to_q.weight", {C, C}, stream);
     k.wo2 = copy_of(b + "attn2.to_out.0.weight", {C, C}, stream);
     k.bo2 = copy_of(b + "attn2.to_out.0.bias", {C}, stream);
-    // GEGLU projection in the 32-row value/gate interleave
+    // GEGLU projection in the 4-row value/gate interleave
     void* w1 = take((size_t)8 * C * C);
     void* b1 = take((size_t)8 * C);
     const Src& sw = src(b + "ff.net.0.proj.weight", {8 * C, C});

@@ -333,7 +333,7 @@ def linear_vt(x: torch.Tensor, w: torch.Tensor, vt_col0: int, tokens: int, bias=
 
 
 def pack_geglu(w: torch.Tensor, b: Optional[torch.Tensor]):
-    """[2d, K] value-first GEGLU projection -> 16-row interleave for ACT_GEGLU."""
+    """[2d, K] value-first GEGLU projection -> 4-row value/gate interleave for ACT_GEGLU."""
     two_d, K = w.shape
     d = two_d // 2
     wo = torch.empty_like(w)

@@ -174,9 +174,9 @@ int dlm_gemm_set_variant(int variant);
 /* Epilogue activation codes. */
 #define DLM_ACT_NONE 0
 #define DLM_ACT_SILU 1
-/* GEGLU: the weight rows (and bias) are interleaved in blocks of 32
- * (32 value rows, then the 32 matching gate rows, see dlm_geglu_pack_fp16);
- * the output has N/2 columns: out = value * gelu_erf(gate).  N % 64 == 0. */
+/* GEGLU: the weight rows (and bias) are interleaved in groups of 4
+ * (4 value rows, then the 4 matching gate rows, see dlm_geglu_pack_fp16);
+ * the output has N/2 columns: out = value * gelu_erf(gate).  N % 16 == 0. */
 #define DLM_ACT_GEGLU 2
 #define DLM_ACT_GELU 3
 
@@ -215,8 +215,9 @@ int dlm_linear_f32out_fp16(const void* X, int lda, const void* W, int ldw, const
                            float alpha, float beta, int act, void* stream);
 
 /* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
- * diffusers stores them) into the 32-row interleave DLM_ACT_GEGLU expects
- * (d % 32 == 0). */
+ * diffusers stores them) into the 4-row value/gate interleave DLM_ACT_GEGLU
+ * expects: packed row 8q+s holds value row 4q+s (s < 4) or gate row
+ * d+4q+s-4 (d % 4 == 0). */
 int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias_out,
                         int d, int K, void* stream);
 
