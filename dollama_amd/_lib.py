@@ -127,6 +127,7 @@ HIP_SIGNATURES = {
     "dlm_image_to_rgb8": (I, [P, P, I, I, I, P]),
     "dlm_softmax_rows_f32_fp16": (I, [P, LL, P, LL, I, I, P]),
     "dlm_gemm_force_tile": (I, [I]),
+    "dlm_gemm_override_shape": (I, [I, I, I, I, I]),
     "dlm_gemm_force_split": (I, [I]),
     "dlm_gemm_set_variant": (I, [I]),
 }

@@ -22,6 +22,7 @@
 // sources, nearest-2x upsampling, a second 1x1 segment) for convolutions.
 #include <algorithm>
 #include <map>
+#include <vector>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -1134,8 +1135,37 @@ static bool dma_operand_ok(const ConvDesc& d) {
 }
 
 template <class Desc>
+static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
+                            hipStream_t s);
+
+// Tuning aid: per-shape tile / split overrides (dlm_gemm_override_shape),
+// matched on (M, N, K); single-threaded tuning use only.
+struct ShapeOverride {
+  int M, N, K, tile, split;
+};
+static std::vector<ShapeOverride> g_overrides;
+
+template <class Desc>
 static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                        hipStream_t s) {
+  if (!g_overrides.empty()) {
+    for (const ShapeOverride& o : g_overrides)
+      if (o.M == M && o.N == N && o.K == bd.K) {
+        const int t = g_forced_tile, sp = g_forced_split;
+        g_forced_tile = o.tile;
+        g_forced_split = o.split;
+        const int st = launch_gemm_impl(ad, bd, ep, M, N, s);
+        g_forced_tile = t;
+        g_forced_split = sp;
+        return st;
+      }
+  }
+  return launch_gemm_impl(ad, bd, ep, M, N, s);
+}
+
+template <class Desc>
+static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
+                            hipStream_t s) {
   constexpr int kCUs = 256;
   if ((ep.y_f32 || ep.res_f32) && (ep.vt || ep.act == DLM_ACT_GEGLU))
     return fail(DLM_ERR_UNSUPPORTED, "fp32 output/residual with a GEGLU or V^T epilogue");
@@ -1167,12 +1197,14 @@ static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int
       // Measured on the UNet's shapes (warmed-up clocks, N(0,1) data):
       // 8-wave tiles (two waves per SIMD) everywhere.  128x128 tiles: two
       // slices in flight when two workgroups share a CU, four when the grid
-      // leaves CUs with one.  GEGLU takes the same tiles (its value/gate
-      // pairs sit in lanes 16 apart, so any 16-column-multiple wave works):
-      // 128x128 two-slice 71 / 81 us on 2048x10240x1280 / 8192x5120x640,
-      // against 77 / 90 us for the 256x128 three-slice tiles the earlier
-      // 64-column pairing needed.
+      // leaves CUs with one.  GEGLU can take any tile (its value/gate pairs
+      // sit in lanes 16 apart, so any 16-column-multiple wave works).
       const long long t128 = ceil_div(M, 128) * ceil_div(N, 128);
+      // GEGLU FF1 (2048x10240 and 8192x5120, K 1280 / 640): 256x160 tiles,
+      // three-slice ring, measured in the whole UNet step in one process:
+      // 25.3 ms against 26.0 (128x128) and 26.7 (256x128)
+      if (ep.act == DLM_ACT_GEGLU && N % 160 == 0 && ceil_div(M, 256) * (N / 160) >= kCUs)
+        return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s);
       // Output widths that are multiples of 160 (SDXL's 320 / 640 / 1280
       // channels): 160-column tiles give whole waves of tiles on 256 CUs
       // where 128-column tiles leave a partial wave; few tiles with a long K
@@ -1756,6 +1788,22 @@ extern "C" int dlm_gemm_set_variant(int variant) {
 extern "C" int dlm_gemm_force_split(int splits) {
   DLM_REQUIRE(splits >= 0 && splits <= 64, "splits must be in [0, 64]");
   dlm::g_forced_split = splits;
+  return DLM_OK;
+}
+
+extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits) {
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 26 && splits >= 0 && splits <= 64, "bad tile / split");
+  if (M == 0 && N == 0 && K == 0) {
+    dlm::g_overrides.clear();
+    return DLM_OK;
+  }
+  auto& v = dlm::g_overrides;
+  for (size_t i = 0; i < v.size(); ++i)
+    if (v[i].M == M && v[i].N == N && v[i].K == K) {
+      v.erase(v.begin() + i);
+      break;
+    }
+  if (tile_id != 0 || splits != 0) v.push_back({M, N, K, tile_id, splits});
   return DLM_OK;
 }
 

@@ -162,6 +162,10 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
  * 25 64x160 32x80 2, 26 128x80 16x80 5.  Splits apply to the LDS-DMA core
  * only. */
 int dlm_gemm_force_tile(int tile_id);
+/* Same override for GEMMs / convs of one shape (M, N = output columns,
+ * K = reduction length); tile 0 and splits 0 remove it, M = N = K = 0 clears
+ * every override.  Single-threaded tuning use. */
+int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits);
 int dlm_gemm_force_split(int splits);
 /* Tuning aid: select alternative tile heuristics (0 = default; bit 0 = no
  * 160-column / split-K rules). */
