@@ -839,7 +839,12 @@ __device__ __forceinline__ void split_coords(int bid, int tiles_m, int tiles_n, 
   tn = rem / gsz;
 }
 
-template <int BM, int BN, int WM, int WN, int NS, class Desc>
+// PF: the first k-step's fragments of slice kt+1 are read from LDS right
+// after the barrier that publishes it, while the second k-step of slice kt
+// (already in registers) runs on the MFMA pipe; the whole ring is filled
+// before the loop and slot kt is refilled (with slice kt+NS) as soon as that
+// barrier proves every wave has read it.
+template <int BM, int BN, int WM, int WN, int NS, bool PF, class Desc>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, SplitArgs sp) {
   constexpr int WAVES_N = BN / WN;
@@ -906,13 +911,67 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
     for (int i = 0; i < IB; ++i) dma_b(st, i, kt);
   };
 
+  constexpr int PRE = PF ? NS : NS - 1;  // slices in flight before the loop
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue_all(s, min(kb + s, ke - 1));
+  for (int s = 0; s < PRE; ++s) issue_all(s, min(kb + s, ke - 1));
 
   // DMA instructions this wave skips per slice (0..2): the vmcnt wait for
-  // "slice kt landed" allows NS-2 later slices of this wave's own requests
+  // "slice kt landed" allows P later slices of this wave's own requests
   const int skips = ((IA * NW == GA || wave < GA - (IA - 1) * NW) ? 0 : 1) +
                     ((IB * NW == GB || wave < GB - (IB - 1) * NW) ? 0 : 1);
+#define DLM_WAIT_SLICES(P)                   \
+  do {                                       \
+    if (skips == 0) {                        \
+      DLM_WAIT_VM((P) * (IA + IB));          \
+    } else if (skips == 1) {                 \
+      DLM_WAIT_VM((P) * (IA + IB - 1));      \
+    } else {                                 \
+      DLM_WAIT_VM((P) * (IA + IB - 2));      \
+    }                                        \
+  } while (0)
+  if constexpr (PF) {
+    static_assert(KS == 2, "prefetch form assumes two k-steps per slice");
+    f16x8 f0a[TM], f0b[TN], f1a[TM], f1b[TN];
+    auto rd = [&](const unsigned char DLM_LDS* st, int ks, f16x8 (&fa)[TM], f16x8 (&fb)[TN]) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = frag(st, wm * WM + i * 16 + (lane & 15), ks);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = frag(st + SA, wn * WN + j * 16 + (lane & 15), ks);
+    };
+    auto mma = [&](const f16x8 (&fa)[TM], const f16x8 (&fb)[TN]) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(fb[j], fa[i], acc[i][j]);
+    };
+    DLM_WAIT_SLICES(NS - 1);  // slice kb
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    rd(smem, 0, f0a, f0b);
+    for (int kt = kb; kt < ke; ++kt) {
+      const int rel = kt - kb;
+      const int slot = rel % NS;
+      __builtin_amdgcn_sched_barrier(0);
+      rd(smem + slot * STAGE, 1, f1a, f1b);
+      mma(f0a, f0b);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 1 < ke) {
+        // this wave's reads of the slot are complete before the barrier
+        // after which another wave may refill it
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        DLM_WAIT_SLICES(NS - 2);             // slice kt+1
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        rd(smem + ((rel + 1) % NS) * STAGE, 0, f0a, f0b);
+        issue_all(slot, min(kt + NS, ke - 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f1a, f1b);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
   for (int kt = kb; kt < ke; ++kt) {
     if (skips == 0) {
       DLM_WAIT_VM((NS - 2) * (IA + IB));
@@ -955,6 +1014,8 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  }
+#undef DLM_WAIT_SLICES
   DLM_WAIT_VM(0);  // no DMA may still be writing this workgroup's LDS at exit
 
   if (sp.S > 1) {
@@ -1073,7 +1134,7 @@ static const SplitWorkspace* split_workspace(hipStream_t s) {
 static int g_forced_split = 0;
 static int g_variant = 0;  // tuning aid: bits select alternative heuristics
 
-template <int BM, int BN, int WM, int WN, int NS, class Desc>
+template <int BM, int BN, int WM, int WN, int NS, bool PF = false, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                       hipStream_t s, int S = 1) {
   static_assert(NS * (BM + BN) * BK * 2 <= 160 * 1024, "LDS ring larger than 160 KiB");
@@ -1092,8 +1153,8 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   }
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
   const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
-  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, Desc>), dim3(grid), dim3(NT), 0, s, ad, bd,
-                     ep, tiles_m, tiles_n, sp);
+  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, Desc>), dim3(grid), dim3(NT), 0, s, ad,
+                     bd, ep, tiles_m, tiles_n, sp);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -1191,6 +1252,14 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       case 24: return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
       case 25: return launch_dma<64, 160, 32, 80, 2>(ad, bd, ep, M, N, s);
       case 26: return launch_dma<128, 80, 16, 80, 5>(ad, bd, ep, M, N, s);
+      case 27: return launch_dma<128, 80, 16, 80, 5, true>(ad, bd, ep, M, N, s);
+      case 28: return launch_dma<256, 160, 64, 80, 3, true>(ad, bd, ep, M, N, s);
+      case 29: return launch_dma<128, 128, 64, 32, 2, true>(ad, bd, ep, M, N, s);
+      case 30: return launch_dma<128, 160, 32, 80, 4, true>(ad, bd, ep, M, N, s);
+      case 31: return launch_dma<128, 160, 32, 80, 3, true>(ad, bd, ep, M, N, s);
+      case 32: return launch_dma<256, 128, 64, 64, 3, true>(ad, bd, ep, M, N, s);
+      case 33: return launch_dma<128, 128, 64, 32, 4, true>(ad, bd, ep, M, N, s);
+      case 34: return launch_dma<128, 64, 64, 32, 2, true>(ad, bd, ep, M, N, s);
       default: break;
     }
     if (g_forced_tile == 0) {
@@ -1200,17 +1269,22 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       // leaves CUs with one.  GEGLU can take any tile (its value/gate pairs
       // sit in lanes 16 apart, so any 16-column-multiple wave works).
       const long long t128 = ceil_div(M, 128) * ceil_div(N, 128);
+      const bool pf = !(g_variant & 2);
       // GEGLU FF1 (2048x10240 and 8192x5120, K 1280 / 640): 256x160 tiles,
       // three-slice ring, measured in the whole UNet step in one process:
-      // 25.3 ms against 26.0 (128x128) and 26.7 (256x128)
+      // 25.3 ms against 26.0 (128x128) and 26.7 (256x128); the fragment-
+      // prefetch form saves a further ~2 us (2048x10240) and ~12 us
+      // (8192x5120) per launch
       if (ep.act == DLM_ACT_GEGLU && N % 160 == 0 && ceil_div(M, 256) * (N / 160) >= kCUs)
-        return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s);
+        return pf ? launch_dma<256, 160, 64, 80, 3, true>(ad, bd, ep, M, N, s)
+                  : launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s);
       // Output widths that are multiples of 160 (SDXL's 320 / 640 / 1280
       // channels): 160-column tiles give whole waves of tiles on 256 CUs
       // where 128-column tiles leave a partial wave; few tiles with a long K
       // are split-K so every CU gets work.  Choices measured per UNet level
-      // (B=2): 32768x320 convs 256x160 (4 splits from 80 slices on), 8192 rows
-      // 128x160 up to 100 slices and 256x160 x2 splits beyond, 2048 rows
+      // (B=2): 32768x320 convs 256x160 (four splits from 80 slices on measured
+      // the same as none; 8192x1280x11520 is ~130 us faster unsplit), 8192
+      // rows 128x160 up to 100 slices and 256x160 x2 splits beyond, 2048 rows
       // 128x160 x2 splits from 44 slices, 256x160 x4 from 300.  Two splits of
       // a grid that already fills the chip measured slower than one or four.
       const int nk = (int)ceil_div(bd.K, BK);
@@ -1224,7 +1298,7 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       if (!ep.vt && N % 160 == 0 && N <= 1280 && !(g_variant & 1)) {
         const long long t256 = ceil_div(M, 256) * (N / 160), t160 = ceil_div(M, 128) * (N / 160);
         if (t256 >= kCUs)
-          return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, nk >= 80 ? 4 : 1);
+          return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, !pf && nk >= 80 ? 4 : 1);
         if (t160 >= kCUs) {
           if (nk <= 100) return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
           return launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s, 2);
@@ -1243,8 +1317,12 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
         // (fewer operand bytes per MFMA; the im2col loader is the costlier one)
         if (std::is_same<Desc, ConvDesc>::value && t128 >= kCUs && t128 < 4 * kCUs)
           return launch_dma<256, 128, 64, 64, 3>(ad, bd, ep, M, N, s);
-        return t128 >= kCUs ? launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s)
-                            : launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
+        // one workgroup's ring of two slices: the prefetch form (2048x3840x1280
+        // QKV ~2 us faster per launch, 8192x1920x640 the same)
+        if (t128 >= kCUs)
+          return pf ? launch_dma<128, 128, 64, 32, 2, true>(ad, bd, ep, M, N, s)
+                    : launch_dma<128, 128, 64, 32, 2>(ad, bd, ep, M, N, s);
+        return launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
       }
       if (ep.vt)  // the transposed-V epilogue exists only in the DMA core
         return launch_dma<128, 128, 64, 32, 4>(ad, bd, ep, M, N, s);
@@ -1792,7 +1870,7 @@ extern "C" int dlm_gemm_force_split(int splits) {
 }
 
 extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 26 && splits >= 0 && splits <= 64, "bad tile / split");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 34 && splits >= 0 && splits <= 64, "bad tile / split");
   if (M == 0 && N == 0 && K == 0) {
     dlm::g_overrides.clear();
     return DLM_OK;
@@ -1808,7 +1886,7 @@ extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int spl
 }
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 26, "tile_id must be in [0, 26]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 34, "tile_id must be in [0, 34]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

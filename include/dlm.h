@@ -159,7 +159,11 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
  * 16 256x128 64x64 2, 17 128x128 32x64 4, 18 128x128 64x32 5,
  * 19 256x128 64x64 3, 20 128x64 64x32 6, 21 256x160 64x80 3,
  * 22 128x160 32x80 3, 23 128x160 64x80 2, 24 128x160 32x80 4,
- * 25 64x160 32x80 2, 26 128x80 16x80 5.  Splits apply to the LDS-DMA core
+ * 25 64x160 32x80 2, 26 128x80 16x80 5; 27-34 the same core with the next
+ * slice's first fragments read during the current slice's last MFMAs:
+ * 27 128x80 16x80 5, 28 256x160 64x80 3, 29 128x128 64x32 2,
+ * 30 128x160 32x80 4, 31 128x160 32x80 3, 32 256x128 64x64 3,
+ * 33 128x128 64x32 4, 34 128x64 64x32 2.  Splits apply to the LDS-DMA core
  * only. */
 int dlm_gemm_force_tile(int tile_id);
 /* Same override for GEMMs / convs of one shape (M, N = output columns,
@@ -168,7 +172,8 @@ int dlm_gemm_force_tile(int tile_id);
 int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits);
 int dlm_gemm_force_split(int splits);
 /* Tuning aid: select alternative tile heuristics (0 = default; bit 0 = no
- * 160-column / split-K rules). */
+ * 160-column / split-K rules; bit 1 = no fragment-prefetch forms, four
+ * splits for 256x160 grids that fill the chip). */
 int dlm_gemm_set_variant(int variant);
 
 /* ------------------------------------------------------------------ */

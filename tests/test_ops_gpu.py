@@ -55,6 +55,39 @@ def test_linear_geglu(gpu, M, d, K):
     assert_close(y, R.geglu(R.linear(x, w, b)), f"geglu {M}x{d}x{K}")
 
 
+@pytest.mark.parametrize("tile", list(range(8, 35)))
+def test_dma_tile_configs(gpu, tile):
+    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-34, the
+    fragment-prefetch forms 27-34 included), whole and split-K, on ragged
+    shapes with a K tail: bias + SiLU + residual, GEGLU, and a 3x3 conv with
+    residual."""
+    from dollama_amd import _lib
+    announce(f"forced DMA tile {tile}")
+    M, N, K = 300, 240, 712
+    x, w = randn((M, K), 13), randn((N, K), 14, std=0.04)
+    b, r = randn((N,), 15, std=0.1), randn((M, N), 16)
+    ref = R.silu(R.linear(x, w, b)) + r
+    wg, bg = randn((2 * 80, K), 17, std=0.04), randn((2 * 80,), 18, std=0.01)
+    xc, wc = randn((2, 128, 12, 10), 19), randn((160, 128, 3, 3), 20, std=0.03)
+    rc = randn((2, 160, 12, 10), 21)
+    try:
+        _lib.call("dlm_gemm_force_tile", tile)
+        for splits in (0, 3):
+            _lib.call("dlm_gemm_force_split", splits)
+            y = ops.linear(to_gpu(x), to_gpu(w), bias=to_gpu(b), residual=to_gpu(r), act=ops.ACT_SILU)
+            assert_close(y, ref, f"tile {tile} splits {splits} linear+bias+silu+res {M}x{N}x{K}")
+            yc = ops.conv2d_nhwc(ops.nchw_to_nhwc(to_gpu(xc)), ops.pack_conv_weight(to_gpu(wc)), KH=3, KW=3,
+                                 residual=ops.nchw_to_nhwc(to_gpu(rc)))
+            assert_close(ops.nhwc_to_nchw(yc), R.conv2d(xc, wc, None) + rc, f"tile {tile} splits {splits} conv")
+        _lib.call("dlm_gemm_force_split", 0)
+        wp, bp = ops.pack_geglu(to_gpu(wg), to_gpu(bg))
+        yg = ops.linear(to_gpu(x), wp, bias=bp, act=ops.ACT_GEGLU)
+        assert_close(yg, R.geglu(R.linear(x, wg, bg)), f"tile {tile} geglu")
+    finally:
+        _lib.call("dlm_gemm_force_tile", 0)
+        _lib.call("dlm_gemm_force_split", 0)
+
+
 @pytest.mark.parametrize("transA,transB", [(False, True), (False, False), (True, True), (True, False)])
 def test_gemm_reference_api(gpu, transA, transB):
     M, N, K = 70, 50, 36
