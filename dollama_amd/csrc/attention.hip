@@ -280,14 +280,19 @@ constexpr int kFaOOB = (int)0x80000000;
 // kt+2: one tile of DMA latency hidden, three buffers.  Full tiles carry no
 // masking code; the rescale is a real (rare) branch; the row sum is taken
 // over the fp16 P the MFMA consumes, two terms per dot2.
-__global__ void __launch_bounds__(256) flash_vt_pipe_kernel(FlashVtParams p) {
+// NWV waves per workgroup (4: 128 queries; 2: 64 queries for grids that
+// would otherwise leave SIMDs with a single wave).  Each wave issues 8 / NWV
+// of the 8-row DMA groups of every K and V^T tile.
+template <int NWV>
+__global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p) {
+  constexpr int DI = 8 / NWV;  // DMA instructions per wave per operand tile
   __shared__ __attribute__((aligned(1024))) unsigned char smem_g[FA_NS * FA_STAGE];
   unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_g;
   const int b = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;
-  const int q0 = blockIdx.x * 128 + wave * 32;
+  const int q0 = blockIdx.x * (NWV * 32) + wave * 32;
 
   f16x8 qf[4];
   {
@@ -300,10 +305,10 @@ __global__ void __launch_bounds__(256) flash_vt_pipe_kernel(FlashVtParams p) {
 
   const i32x4 rk = fa_rsrc(p.k, p.k_bytes);
   const i32x4 rv = fa_rsrc(p.vt, p.vt_bytes);
-  int koff[2], kkey[2], voff[2], vkey[2];
+  int koff[DI], kkey[DI], voff[DI], vkey[DI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (wave * 2 + i) * 8 + (lane >> 3);
+  for (int i = 0; i < DI; ++i) {
+    const int r = (wave * DI + i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     kkey[i] = fa_perm(r);
     koff[i] = (int)((b * p.k_sb + h * p.k_sh + (long long)kkey[i] * p.k_ss + c * 8) * 2);
@@ -314,14 +319,14 @@ __global__ void __launch_bounds__(256) flash_vt_pipe_kernel(FlashVtParams p) {
   auto issue = [&](int buf, int kt) {
     unsigned char DLM_LDS* st = smem + buf * FA_STAGE;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < DI; ++i) {
       const int key = kt * FA_TK + kkey[i];
-      fa_dma16(rk, st + (wave * 2 + i) * 1024, key < p.Sk ? koff[i] + kt * kstep : kFaOOB);
+      fa_dma16(rk, st + (wave * DI + i) * 1024, key < p.Sk ? koff[i] + kt * kstep : kFaOOB);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < DI; ++i) {
       const int key = kt * FA_TK + vkey[i];
-      fa_dma16(rv, st + FA_TILE + (wave * 2 + i) * 1024, key < p.Sk ? voff[i] + kt * (FA_TK * 2) : kFaOOB);
+      fa_dma16(rv, st + FA_TILE + (wave * DI + i) * 1024, key < p.Sk ? voff[i] + kt * (FA_TK * 2) : kFaOOB);
     }
   };
   auto frag = [&](const unsigned char DLM_LDS* st, int row, int chunk) -> f16x8 {
@@ -406,7 +411,7 @@ __global__ void __launch_bounds__(256) flash_vt_pipe_kernel(FlashVtParams p) {
 
   // prologue: tile 0 published, its scores issued
   if (nkt > 1) {
-    FA_WAIT_VM(4);
+    FA_WAIT_VM(2 * DI);  // tile 1's requests may still be in flight
   } else {
     FA_WAIT_VM(0);
   }
@@ -491,9 +496,16 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   p.vt_bytes = (unsigned)a->vt_bytes;
   // One 32-query block per wave: the softmax is VALU work that only other
   // waves' MFMAs can hide, so more waves beat sharing K/V fragments between
-  // two query blocks (2x4096^2 x10 heads: 144 us vs 170 us).
-  const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
-  hipLaunchKernelGGL(flash_vt_pipe_kernel, grid, dim3(256), 0, s, p);
+  // two query blocks (2x4096^2 x10 heads: 144 us vs 170 us).  Grids of fewer
+  // than two 128-query workgroups per CU (1024 tokens x 20 heads x 2) take
+  // 64-query workgroups: twice the K/V staging, but waves spread evenly.
+  if ((long long)((a->Sq + 127) / 128) * a->H * a->B < 512) {
+    const dim3 grid((a->Sq + 63) / 64, a->H, a->B);
+    hipLaunchKernelGGL(flash_vt_pipe_kernel<2>, grid, dim3(128), 0, s, p);
+  } else {
+    const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
+    hipLaunchKernelGGL(flash_vt_pipe_kernel<4>, grid, dim3(256), 0, s, p);
+  }
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
