@@ -167,8 +167,14 @@ __device__ __forceinline__ void chan_merge(double& n, double& mean, double& m2, 
   n = tot;
 }
 
-// One wave per (n, group): merge the chunk partials in fp64 (Chan), emit
-// per-channel scale = gamma*rstd and shift = beta - mean*scale.
+// One wave per (n, group): combine the chunk partials (count n_b, mean m_b,
+// M2_b) in fp64 by the two-pass decomposition
+//   mean = sum(n_b m_b) / sum(n_b),  M2 = sum(M2_b + n_b (m_b - mean)^2),
+// which needs no division per chunk (a pairwise Chan merge needs one), then
+// emit per-channel scale = gamma*rstd and shift = beta - mean*scale.  Each
+// lane sums its chunks in order and the xor butterfly adds identical operand
+// pairs on both partners, so every lane ends with the same, launch-invariant
+// result.
 __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, int C, int G,
                                    int chunk, int chunks, const f16* __restrict__ gamma,
                                    const f16* __restrict__ beta, float eps,
@@ -176,26 +182,29 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
   const int n = blockIdx.x / G, g = blockIdx.x % G;
   const int lane = threadIdx.x;
   const int cpg = C / G;
-  double cnt = 0.0, mean = 0.0, m2 = 0.0;
+  const float2* pg = partial + (size_t)n * chunks * G + g;
+  double cnt = 0.0, s1 = 0.0;
   for (int chn = lane; chn < chunks; chn += 64) {
-    const float2 q = partial[((size_t)n * chunks + chn) * G + g];
+    const float2 q = pg[(size_t)chn * G];
     const double nb = (double)(min(HW, (chn + 1) * chunk) - chn * chunk) * cpg;
-    chan_merge(cnt, mean, m2, nb, (double)q.x, (double)q.y);
+    cnt += nb;
+    s1 = fma(nb, (double)q.x, s1);
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const double nb = __shfl_xor(cnt, o, 64);
-    const double mb = __shfl_xor(mean, o, 64);
-    const double qb = __shfl_xor(m2, o, 64);
-    // merge in a lane-order-independent way: lower lane id's data first
-    if ((lane & o) == 0) {
-      chan_merge(cnt, mean, m2, nb, mb, qb);
-    } else {
-      double n0 = nb, m0 = mb, q0 = qb;
-      chan_merge(n0, m0, q0, cnt, mean, m2);
-      cnt = n0; mean = m0; m2 = q0;
-    }
+    cnt += __shfl_xor(cnt, o, 64);
+    s1 += __shfl_xor(s1, o, 64);
   }
+  const double mean = cnt > 0.0 ? s1 / cnt : 0.0;
+  double m2 = 0.0;
+  for (int chn = lane; chn < chunks; chn += 64) {
+    const float2 q = pg[(size_t)chn * G];
+    const double nb = (double)(min(HW, (chn + 1) * chunk) - chn * chunk) * cpg;
+    const double d = (double)q.x - mean;
+    m2 += (double)q.y + nb * d * d;
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m2 += __shfl_xor(m2, o, 64);
   const double var = cnt > 0.0 ? fmax(m2 / cnt, 0.0) : 0.0;
   const float rstd = (float)(1.0 / sqrt(var + (double)eps));
   for (int ci = lane; ci < cpg; ci += 64) {
@@ -290,13 +299,24 @@ layer_norm_kernel(const f16* __restrict__ in, const f16* __restrict__ gamma,
   if (row >= rows) return;
   const int S = C / 8;
   const f16* x = in + (size_t)row * C;
+  // the row and its gamma / beta vectors are requested together, so the
+  // affine operands arrive while the two reductions run
   float v[VPL][8];
-  float sum = 0.0f;
+  f16x8 gh[VPL], bh[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int s = lane + 64 * j;
     if (s < S) {
       load8(x + s * 8, v[j]);
+      if (gamma) gh[j] = *reinterpret_cast<const f16x8*>(gamma + s * 8);
+      if (beta) bh[j] = *reinterpret_cast<const f16x8*>(beta + s * 8);
+    }
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int s = lane + 64 * j;
+    if (s < S) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) sum += v[j][i];
     }
@@ -319,18 +339,13 @@ layer_norm_kernel(const f16* __restrict__ in, const f16* __restrict__ gamma,
   for (int j = 0; j < VPL; ++j) {
     const int s = lane + 64 * j;
     if (s < S) {
-      float g[8], bb[8];
-      if (gamma) load8(gamma + s * 8, g);
-      else
-#pragma unroll
-        for (int i = 0; i < 8; ++i) g[i] = 1.0f;
-      if (beta) load8(beta + s * 8, bb);
-      else
-#pragma unroll
-        for (int i = 0; i < 8; ++i) bb[i] = 0.0f;
       f16x8 y;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = (f16)((v[j][i] - mean) * rstd * g[i] + bb[i]);
+      for (int i = 0; i < 8; ++i) {
+        const float gi = gamma ? (float)gh[j][i] : 1.0f;
+        const float bi = beta ? (float)bh[j][i] : 0.0f;
+        y[i] = (f16)((v[j][i] - mean) * rstd * gi + bi);
+      }
       *reinterpret_cast<f16x8*>(out + (size_t)row * C + s * 8) = y;
     }
   }

@@ -219,6 +219,23 @@ def test_group_norm_nhwc_concat(gpu):
     assert_close(ops.nhwc_to_nchw(y), ref, "group_norm nhwc concat")
 
 
+def test_group_norm_large_offset(gpu):
+    """Mean 40 against std 0.5 (a ratio of 80): the chunk statistics must be
+    combined without cancellation (E[x^2] - mean^2 in fp32 would lose about
+    four digits here); the reference runs in float64 on the same fp16 values.
+    A second call on the same input gives the same bits."""
+    N, C, H, W, G = 2, 640, 64, 64, 32
+    announce("group_norm nhwc, mean 40 / std 0.5")
+    x = randn((N, C, H, W), 84, std=0.5, mean=40.0)
+    gm, bt = randn((C,), 85, std=0.3, mean=1.0), randn((C,), 86, std=0.3)
+    xg = ops.nchw_to_nhwc(to_gpu(x))
+    y = ops.group_norm_nhwc(xg, to_gpu(gm), to_gpu(bt), G, 1e-5, False)
+    y2 = ops.group_norm_nhwc(xg, to_gpu(gm), to_gpu(bt), G, 1e-5, False)
+    assert torch.equal(y, y2)
+    ref = R.group_norm(x.double(), G, gm.double(), bt.double(), 1e-5).float()
+    assert_close(ops.nhwc_to_nchw(y), ref, "group_norm large offset")
+
+
 # ------------------------------------------------------------- LayerNorm ---
 @pytest.mark.parametrize("rows,C", [(8192, 640), (2048, 1280), (77, 2048), (5, 100)])
 def test_layer_norm(gpu, rows, C):
