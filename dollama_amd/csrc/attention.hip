@@ -499,7 +499,9 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   // two query blocks (2x4096^2 x10 heads: 144 us vs 170 us).  Grids of fewer
   // than two 128-query workgroups per CU (1024 tokens x 20 heads x 2) take
   // 64-query workgroups: twice the K/V staging, but waves spread evenly.
-  if ((long long)((a->Sq + 127) / 128) * a->H * a->B < 512) {
+  // Cross attention (every key in at most two tiles): always 128-query
+  // workgroups, whose one K/V staging serves twice the queries.
+  if (a->Sk > 2 * FA_TK && (long long)((a->Sq + 127) / 128) * a->H * a->B < 512) {
     const dim3 grid((a->Sq + 63) / 64, a->H, a->B);
     hipLaunchKernelGGL(flash_vt_pipe_kernel<2>, grid, dim3(128), 0, s, p);
   } else {
