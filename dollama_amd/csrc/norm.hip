@@ -216,35 +216,60 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
   }
 }
 
+// Apply: same blocks as the statistics pass (one chunk of one sample's
+// pixels, S * R threads).  A thread owns one 8-channel vector for the whole
+// chunk: its source (concat half), scale and shift are fixed, so they are
+// resolved once and stay in registers, and the loop keeps four pixel rows in
+// flight per thread.
 template <typename T>
 __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
                                 const T* __restrict__ b, int ldb, f16* __restrict__ out,
-                                int ldo, int HW, int C, int total_vec,
+                                int ldo, int HW, int C, int S, int R, int chunk,
                                 const float2* __restrict__ ss, int silu) {
-  const int S = C / 8;
-  for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < total_vec; v += gridDim.x * blockDim.x) {
-    const int row = v / S;  // n*HW + p
-    const int s = v - row * S;
-    const int n = row / HW;
-    const int c = s * 8;
-    const T* src = c < Ca ? a + (size_t)row * lda + c : b + (size_t)row * ldb + (c - Ca);
-    float x[8];
-    load8(src, x);
-    const float4* ssv = reinterpret_cast<const float4*>(ss + (size_t)n * C + c);
-    f16x8 y;
+  const int n = blockIdx.y;
+  const int r = threadIdx.x / S, s = threadIdx.x - r * S;
+  const int c = s * 8;
+  const int p0 = blockIdx.x * chunk;
+  const int p1 = min(HW, p0 + chunk);
+  const T* src;
+  int ld;
+  if (c < Ca) {
+    src = a + c;
+    ld = lda;
+  } else {
+    src = b + (c - Ca);
+    ld = ldb;
+  }
+  src += (size_t)n * HW * ld;
+  f16* dst = out + (size_t)n * HW * ldo + c;
+  float sc[8], sh[8];
+  const float4* ssv = reinterpret_cast<const float4*>(ss + (size_t)n * C + c);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 q = ssv[i];
-      float y0 = x[2 * i] * q.x + q.y;
-      float y1 = x[2 * i + 1] * q.z + q.w;
-      if (silu) {
-        y0 = silu_f(y0);
-        y1 = silu_f(y1);
+  for (int i = 0; i < 4; ++i) {
+    const float4 q = ssv[i];
+    sc[2 * i] = q.x;
+    sh[2 * i] = q.y;
+    sc[2 * i + 1] = q.z;
+    sh[2 * i + 1] = q.w;
+  }
+  for (int p = p0 + r; p < p1; p += 4 * R) {
+    float x[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (p + u * R < p1) load8(src + (size_t)(p + u * R) * ld, x[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (p + u * R < p1) {
+        f16x8 y;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float t = x[u][i] * sc[i] + sh[i];
+          if (silu) t = silu_f(t);
+          y[i] = (f16)t;
+        }
+        *reinterpret_cast<f16x8*>(dst + (size_t)(p + u * R) * ldo) = y;
       }
-      y[2 * i] = (f16)y0;
-      y[2 * i + 1] = (f16)y1;
     }
-    *reinterpret_cast<f16x8*>(out + (size_t)row * ldo + c) = y;
   }
 }
 
@@ -270,9 +295,8 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
                      p.chunks, (const f16*)gamma, (const f16*)beta, eps, ss);
   DLM_LAUNCH_CHECK();
-  const int blocks = (int)std::min<long long>((total_vec + 255) / 256, 8192);
-  hipLaunchKernelGGL(gn_apply_kernel<T>, dim3(blocks), dim3(256), 0, s, a, C_a, ld_a, b, ld_b,
-                     (f16*)out, ld_out, HW, C, (int)total_vec, ss, silu);
+  hipLaunchKernelGGL(gn_apply_kernel<T>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a,
+                     b, ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss, silu);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
