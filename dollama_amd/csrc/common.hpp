@@ -92,8 +92,11 @@ namespace dlm {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int hip_fail(hipError_t e, const char* what, const char* file, int line);
-size_t& scratch_bytes_ref();
-void* scratch(size_t bytes, int slot, hipStream_t stream, int* status);
+// Grow-only staging buffer `slot` of the current device for `stream`, used by
+// the reference-layout entry points.  Growing it synchronises the device and
+// frees the old block, so those entry points are not capturable into a graph
+// until their slots have reached size.
+void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status);
 }  // namespace dlm
 
 #define DLM_HIP(expr)                                                          \

@@ -129,7 +129,7 @@ struct ConvParams {
   int C0a, C0, ld0a, ld0b;
   int H, W;    // stored source resolution
   int Hv, Wv;  // resolution the taps index (2H x 2W when upsampling)
-  int KW, stride, pad, up;
+  int KW, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, up;  // up: stride 1, dil 1 only
   int K0;      // KH*KW*C0
   // segment 1: 1x1 conv over concat(src1a[:C1a], src1b[:C1-C1a]) at output res
   const f16* s1a;
@@ -159,8 +159,8 @@ struct ConvDesc : ConvParams {
           const int oh = p / d.Wo;
           const int ow = p - oh * d.Wo;
           pbase[i] = n * d.H * d.W;
-          ihb[i] = oh * d.stride - d.pad;
-          iwb[i] = ow * d.stride - d.pad;
+          ihb[i] = oh * d.stride_h - d.pad_h;
+          iwb[i] = ow * d.stride_w - d.pad_w;
         } else {
           pbase[i] = -1;
           ihb[i] = 0;
@@ -200,7 +200,7 @@ struct ConvDesc : ConvParams {
         }
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-          int ih = ihb[i] + kh, iw = iwb[i] + kw;
+          int ih = ihb[i] + kh * d.dil_h, iw = iwb[i] + kw * d.dil_w;
           const bool ok = kin && pbase[i] >= 0 && (unsigned)ih < (unsigned)d.Hv &&
                           (unsigned)iw < (unsigned)d.Wv;
           if (d.up) {
@@ -600,7 +600,7 @@ struct ConvDma {
   // uniform parameters
   const f16 *s0a, *s0b, *s1a, *s1b;
   unsigned bytes0a, bytes0b, bytes1a, bytes1b;
-  int C0, C0a, ld0a, ld0b, C1, C1a, ld1a, ld1b, K0, KW, Hv, Wv, W, up, M;
+  int C0, C0a, ld0a, ld0b, C1, C1a, ld1a, ld1b, K0, KW, Hv, Wv, W, up, M, dil_h, dil_w;
   // per-slice state
   i32x4 rs;
   int seg, kh, kw, ld, cbase;
@@ -608,7 +608,7 @@ struct ConvDma {
       : s0a(d.s0a), s0b(d.s0b), s1a(d.s1a), s1b(d.s1b), bytes0a(d.bytes0a), bytes0b(d.bytes0b),
         bytes1a(d.bytes1a), bytes1b(d.bytes1b), C0(d.C0), C0a(d.C0a), ld0a(d.ld0a), ld0b(d.ld0b),
         C1(d.C1), C1a(d.C1a), ld1a(d.ld1a), ld1b(d.ld1b), K0(d.K0), KW(d.KW), Hv(d.Hv), Wv(d.Wv),
-        W(d.W), up(d.up), M(d.M) {
+        W(d.W), up(d.up), M(d.M), dil_h(d.dil_h), dil_w(d.dil_w) {
 #pragma unroll
     for (int i = 0; i < I; ++i) {
       const int row = dma_row(nw, i, wave, lane);
@@ -621,8 +621,8 @@ struct ConvDma {
       const int oh = q / d.Wo;
       const int ow = q - oh * d.Wo;
       pbase[i] = m < d.M ? n * d.H * d.W : -1;
-      ihb[i] = oh * d.stride - d.pad;
-      iwb[i] = ow * d.stride - d.pad;
+      ihb[i] = oh * d.stride_h - d.pad_h;
+      iwb[i] = ow * d.stride_w - d.pad_w;
     }
   }
   // Slices are requested in order (kb, kb+1, ..., then the last one
@@ -660,8 +660,8 @@ struct ConvDma {
     rs = dma_rsrc(src, bytes);
     ld = rfl(s1 ? pick(isa1, ld1a, ld1b) : pick(isa0, ld0a, ld0b));
     cbase = rfl(s1 ? pick(isa1, cs, cs - C1a) : pick(isa0, cur_c, cur_c - C0a));
-    kh = rfl(s1 ? cs : cur_kh);
-    kw = rfl(s1 ? 0 : cur_kw);
+    kh = rfl(s1 ? cs : cur_kh * dil_h);  // segment 0: tap offset in input rows
+    kw = rfl(s1 ? 0 : cur_kw * dil_w);
     seg = rfl(s1 ? 1 : 0);
   }
   // Both segment offsets are always computed and chosen with arithmetic
@@ -1131,8 +1131,11 @@ static const SplitWorkspace* split_workspace(hipStream_t s) {
   return &w;
 }
 
-static int g_forced_split = 0;
-static int g_variant = 0;  // tuning aid: bits select alternative heuristics
+// Tuning aids (dlm_gemm_force_split / _set_variant / _force_tile /
+// _override_shape): thread-local, so they steer only launches made by the
+// thread that set them.
+static thread_local int g_forced_split = 0;
+static thread_local int g_variant = 0;  // bits select alternative heuristics
 
 template <int BM, int BN, int WM, int WN, int NS, bool PF = false, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
@@ -1174,7 +1177,7 @@ static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
 static inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 
 // Tile-shape override for tuning sweeps (0 = automatic choice).
-static int g_forced_tile = 0;
+static thread_local int g_forced_tile = 0;
 
 static bool al8(const void* p) { return ((uintptr_t)p & 7) == 0; }
 
@@ -1200,11 +1203,11 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
                             hipStream_t s);
 
 // Tuning aid: per-shape tile / split overrides (dlm_gemm_override_shape),
-// matched on (M, N, K); single-threaded tuning use only.
+// matched on (M, N, K); per thread, like the other tuning aids.
 struct ShapeOverride {
   int M, N, K, tile, split;
 };
-static std::vector<ShapeOverride> g_overrides;
+static thread_local std::vector<ShapeOverride> g_overrides;
 
 template <class Desc>
 static int launch_gemm(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
@@ -1531,11 +1534,19 @@ int conv_weight_pack(const void* w, void* out, int Cout, int Cin, int KH, int KW
 // ---------------------------------------------------------------------------
 // Convolution (channels-last) host entry.
 // ---------------------------------------------------------------------------
-int conv_nhwc_impl(const dlm_conv_nhwc_args* a, hipStream_t s) {
+// Geometry of one convolution: per-axis stride, zero padding and dilation.
+struct ConvGeom {
+  int sh, sw, ph, pw, dh, dw;
+};
+static inline int conv_out_size(int in, int pad, int dil, int k, int stride) {
+  return (in + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+}
+
+int conv_nhwc_impl(const dlm_conv_nhwc_args* a, const ConvGeom& g, hipStream_t s) {
   const int Hv = a->upsample ? 2 * a->H : a->H;
   const int Wv = a->upsample ? 2 * a->W : a->W;
-  const int Ho = (Hv + 2 * a->pad - a->KH) / a->stride + 1;
-  const int Wo = (Wv + 2 * a->pad - a->KW) / a->stride + 1;
+  const int Ho = conv_out_size(Hv, g.ph, g.dh, a->KH, g.sh);
+  const int Wo = conv_out_size(Wv, g.pw, g.dw, a->KW, g.sw);
   const int C0 = a->C0a + a->C0b;
   const int C1 = a->C1a + a->C1b;
   ConvDesc d{};
@@ -1550,8 +1561,12 @@ int conv_nhwc_impl(const dlm_conv_nhwc_args* a, hipStream_t s) {
   d.Hv = Hv;
   d.Wv = Wv;
   d.KW = a->KW;
-  d.stride = a->stride;
-  d.pad = a->pad;
+  d.stride_h = g.sh;
+  d.stride_w = g.sw;
+  d.pad_h = g.ph;
+  d.pad_w = g.pw;
+  d.dil_h = g.dh;
+  d.dil_w = g.dw;
   d.up = a->upsample;
   d.K0 = a->KH * a->KW * C0;
   d.s1a = (const f16*)a->src1a;
@@ -1675,7 +1690,7 @@ int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, fl
   int lda = K, ldb = K;
   int st = DLM_OK;
   if (transA || Kp != K || !dlm_aligned16(A)) {
-    f16* t = (f16*)scratch((size_t)M * Kp * 2, 0, s, &st);
+    f16* t = (f16*)scratch_slot((size_t)M * Kp * 2, 0, s, &st);
     if (!t) return st;
     DLM_HIP(hipMemsetAsync(t, 0, (size_t)M * Kp * 2, s));
     if (transA) {  // A stored [K, M]
@@ -1690,7 +1705,7 @@ int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, fl
     lda = Kp;
   }
   if (!transB || Kp != K || !dlm_aligned16(B)) {
-    f16* t = (f16*)scratch((size_t)N * Kp * 2, 1, s, &st);
+    f16* t = (f16*)scratch_slot((size_t)N * Kp * 2, 1, s, &st);
     if (!t) return st;
     DLM_HIP(hipMemsetAsync(t, 0, (size_t)N * Kp * 2, s));
     if (!transB) {  // B stored [K, N]
@@ -1803,34 +1818,32 @@ int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* a, void* stream) {
               "operand larger than 2 GiB");
   DLM_REQUIRE((C0 % BK == 0 && a->C0a % BK == 0) || a->C0b == 0,
               "channel concatenation needs 64-aligned channel counts");
-  return conv_nhwc_impl(a, (hipStream_t)stream);
+  return conv_nhwc_impl(a, ConvGeom{a->stride, a->stride, a->pad, a->pad, 1, 1}, (hipStream_t)stream);
 }
 
-// Reference-layout conv (NCHW): stage the input channels-last (padded to a
-// multiple of 8 channels), repack the weight, run the implicit-GEMM kernel
-// and write NCHW straight from the epilogue.
-int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out, int N,
-                    int Cin, int H, int W, int Cout, int KH, int KW, int stride_h, int stride_w,
-                    int pad_h, int pad_w, int dilation_h, int dilation_w, void* stream) {
-  if (N <= 0 || Cin <= 0 || H <= 0 || W <= 0 || Cout <= 0 || KH <= 0 || KW <= 0) return DLM_OK;
-  if (stride_h <= 0 || stride_w <= 0 || dilation_h <= 0 || dilation_w <= 0) return DLM_OK;
-  DLM_REQUIRE(in && weight && out, "NULL operand");
-  if (dilation_h != 1 || dilation_w != 1)
-    return fail(DLM_ERR_UNSUPPORTED, "dlm_conv2d_fp16: dilation != 1 is not supported");
-  if (stride_h != stride_w || pad_h != pad_w)
-    return fail(DLM_ERR_UNSUPPORTED, "dlm_conv2d_fp16: anisotropic stride/pad not supported");
-  const int Ho = (H + 2 * pad_h - KH) / stride_h + 1;
-  const int Wo = (W + 2 * pad_w - KW) / stride_w + 1;
-  if (Ho <= 0 || Wo <= 0) return DLM_OK;
-  hipStream_t s = (hipStream_t)stream;
+}  // extern "C"
+
+namespace dlm {
+
+// Reference-layout conv (NCHW), launch_conv2d (src/kernels/conv2d.cuh:38-40):
+// stage the input channels-last (padded to a multiple of 8 channels) in `x`,
+// repack the weight into `wp`, run the implicit-GEMM kernel and write NCHW
+// straight from the epilogue.  `x` and `wp` are caller-chosen staging
+// buffers of conv2d_nchw_staging() bytes each (every byte that the kernels
+// read is written first).
+static void conv2d_nchw_staging(int N, int Cin, int H, int W, int Cout, int KH, int KW,
+                                size_t* x_bytes, size_t* w_bytes) {
   const int Cp = (Cin + 7) & ~7;
-  const int K = KH * KW * Cp;
-  const int ldw = (K + 7) & ~7;
+  *x_bytes = (size_t)N * H * W * Cp * 2;
+  *w_bytes = (size_t)Cout * (size_t)KH * KW * Cp * 2;
+}
+
+static int conv2d_nchw_run(const void* in, const void* weight, const void* bias, void* out, int N,
+                           int Cin, int H, int W, int Cout, int KH, int KW, const ConvGeom& g,
+                           f16* x, f16* wp, hipStream_t s) {
+  const int Cp = (Cin + 7) & ~7;
+  const int ldw = KH * KW * Cp;  // a multiple of 8
   int st = DLM_OK;
-  f16* x = (f16*)scratch((size_t)N * H * W * Cp * 2, 2, s, &st);
-  if (!x) return st;
-  f16* wp = (f16*)scratch((size_t)Cout * ldw * 2, 3, s, &st);
-  if (!wp) return st;
   if ((st = nchw_to_nhwc(in, x, N, Cin, H * W, Cp, s)) != DLM_OK) return st;
   if ((st = conv_weight_pack(weight, wp, Cout, Cin, KH, KW, Cp, ldw, 0, s)) != DLM_OK) return st;
   dlm_conv_nhwc_args a{};
@@ -1842,8 +1855,8 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
   a.W = W;
   a.KH = KH;
   a.KW = KW;
-  a.stride = stride_h;
-  a.pad = pad_h;
+  a.stride = g.sh;
+  a.pad = g.ph;
   a.weight = wp;
   a.ldw = ldw;
   a.Cout = Cout;
@@ -1852,7 +1865,47 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
   a.ldy = Cout;
   a.out_nchw = 1;
   a.act = DLM_ACT_NONE;
-  return conv_nhwc_impl(&a, s);
+  return conv_nhwc_impl(&a, g, s);
+}
+
+// Argument checks shared by both reference-layout conv entry points.  Returns
+// DLM_OK with *noop set for the reference's silent no-op cases.
+static int conv2d_nchw_check(const void* in, const void* weight, void* out, int N, int Cin, int H,
+                             int W, int Cout, int KH, int KW, const ConvGeom& g, bool* noop) {
+  *noop = true;
+  if (N <= 0 || Cin <= 0 || H <= 0 || W <= 0 || Cout <= 0 || KH <= 0 || KW <= 0) return DLM_OK;
+  if (g.sh <= 0 || g.sw <= 0 || g.dh <= 0 || g.dw <= 0) return DLM_OK;
+  DLM_REQUIRE(in && weight && out, "NULL operand");
+  DLM_REQUIRE(g.ph >= 0 && g.pw >= 0, "negative padding");
+  const int Ho = conv_out_size(H, g.ph, g.dh, KH, g.sh);
+  const int Wo = conv_out_size(W, g.pw, g.dw, KW, g.sw);
+  if (Ho <= 0 || Wo <= 0) return DLM_OK;
+  const int Cp = (Cin + 7) & ~7;
+  DLM_REQUIRE(2LL * N * H * W * Cp < (1LL << 31) && 2LL * Cout * KH * KW * Cp < (1LL << 31),
+              "input or weight larger than 2 GiB");
+  *noop = false;
+  return DLM_OK;
+}
+
+}  // namespace dlm
+
+extern "C" {
+
+int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out, int N,
+                    int Cin, int H, int W, int Cout, int KH, int KW, int stride_h, int stride_w,
+                    int pad_h, int pad_w, int dilation_h, int dilation_w, void* stream) {
+  const ConvGeom g{stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w};
+  bool noop = true;
+  int st = conv2d_nchw_check(in, weight, out, N, Cin, H, W, Cout, KH, KW, g, &noop);
+  if (st != DLM_OK || noop) return st;
+  hipStream_t s = (hipStream_t)stream;
+  size_t xb = 0, wb = 0;
+  conv2d_nchw_staging(N, Cin, H, W, Cout, KH, KW, &xb, &wb);
+  f16* x = (f16*)scratch_slot(xb, 2, s, &st);
+  if (!x) return st;
+  f16* wp = (f16*)scratch_slot(wb, 3, s, &st);
+  if (!wp) return st;
+  return conv2d_nchw_run(in, weight, bias, out, N, Cin, H, W, Cout, KH, KW, g, x, wp, s);
 }
 
 }  // extern "C"

@@ -485,9 +485,9 @@ int dlm_group_norm_fp16(const void* in, const void* gamma, const void* beta, voi
   if (Cp != C)
     return fail(DLM_ERR_UNSUPPORTED, "dlm_group_norm_fp16: C must be a multiple of 8");
   int st = DLM_OK;
-  f16* x = (f16*)scratch((size_t)N * HW * Cp * 2, 4, s, &st);
+  f16* x = (f16*)scratch_slot((size_t)N * HW * Cp * 2, 4, s, &st);
   if (!x) return st;
-  void* ws = scratch(gn_workspace_bytes(N, Cp, HW), 5, s, &st);
+  void* ws = scratch_slot(gn_workspace_bytes(N, Cp, HW), 5, s, &st);
   if (!ws) return st;
   if ((st = nchw_to_nhwc(in, x, N, C, HW, Cp, s)) != DLM_OK) return st;
   if ((st = group_norm_nhwc(x, Cp, Cp, nullptr, 0, gamma, beta, x, Cp, N, HW, Cp, num_groups, eps,

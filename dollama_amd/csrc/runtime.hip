@@ -7,7 +7,9 @@
 // dlm_malloc / dlm_memcpy.
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <tuple>
 #include <vector>
 
 #include "common.hpp"
@@ -31,20 +33,21 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line) {
   return e == hipErrorOutOfMemory ? DLM_ERR_OUT_OF_MEMORY : DLM_ERR_HIP;
 }
 
-// Grow-only per-device, per-slot scratch used by the reference-layout entry
-// points that stage NCHW <-> NHWC copies.  Growth synchronises the device
-// before freeing the old block, so stream-ordered users never see it vanish.
+// Grow-only staging per (device, stream, slot) for the reference-layout entry
+// points that stage NCHW <-> NHWC copies.  Launches on one stream run in order
+// and share that stream's slots; another stream gets its own, so calls on two
+// streams never race on one buffer.  Growth synchronises the device before
+// freeing the old block, so stream-ordered users never see it vanish.
 namespace {
 struct ScratchSlot {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_scratch_mu;
-std::vector<std::vector<ScratchSlot>> g_scratch;  // [device][slot]
+std::map<std::tuple<int, hipStream_t, int>, ScratchSlot> g_scratch;
 }  // namespace
 
-void* scratch(size_t bytes, int slot, hipStream_t stream, int* status) {
-  (void)stream;
+void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status) {
   *status = DLM_OK;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
@@ -52,10 +55,7 @@ void* scratch(size_t bytes, int slot, hipStream_t stream, int* status) {
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1);
-  auto& slots = g_scratch[dev];
-  if ((int)slots.size() <= slot) slots.resize(slot + 1);
-  ScratchSlot& s = slots[slot];
+  ScratchSlot& s = g_scratch[{dev, stream, slot}];
   if (s.bytes >= bytes && s.ptr) return s.ptr;
   if (s.ptr) {
     if (hipDeviceSynchronize() != hipSuccess || hipFree(s.ptr) != hipSuccess) {

@@ -90,9 +90,13 @@ int dlm_event_elapsed_ms(float* ms, void* start, void* stop);
 /* Reference-layout kernel host API (1:1 with src/kernels/ *.cuh)       */
 /* ------------------------------------------------------------------ */
 
-/* conv2d, NCHW fp16, fp32 accumulate, optional bias (NULL = none).
- * Replaces dollama::launch_conv2d (src/kernels/conv2d.cuh:38-40).
- * Groups/dilation other than 1 return DLM_ERR_UNSUPPORTED. */
+/* conv2d, NCHW fp16, fp32 accumulate, optional bias (NULL = none), any
+ * per-axis stride, zero padding and dilation; output size
+ * (H + 2 pad - dilation (KH - 1) - 1) / stride + 1 per axis.
+ * Replaces dollama::launch_conv2d (src/kernels/conv2d.cuh:38-40).  Stages the
+ * input channels-last and the packed weight in library buffers kept per
+ * (device, stream); they grow on first use (hipMalloc after a device
+ * synchronisation), so warm the call before capturing it into a graph. */
 int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out,
                     int N, int Cin, int H, int W, int Cout, int KH, int KW,
                     int stride_h, int stride_w, int pad_h, int pad_w,
@@ -168,7 +172,8 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
 int dlm_gemm_force_tile(int tile_id);
 /* Same override for GEMMs / convs of one shape (M, N = output columns,
  * K = reduction length); tile 0 and splits 0 remove it, M = N = K = 0 clears
- * every override.  Single-threaded tuning use. */
+ * every override.  Like every tuning aid here it is thread-local: it steers
+ * only launches made by the calling thread. */
 int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits);
 int dlm_gemm_force_split(int splits);
 /* Tuning aid: select alternative tile heuristics (0 = default; bit 0 = no

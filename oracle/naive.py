@@ -58,15 +58,21 @@ def _p(a):
     return None if a is None else a.ctypes.data_as(_fp)
 
 
+def _pair(v):
+    return (v, v) if isinstance(v, int) else tuple(v)
+
+
 def conv2d(x, w, b=None, stride=1, pad=1, dilation=1):
+    """stride / pad / dilation: an int or an (h, w) pair."""
     x, w, b = _f32(x), _f32(w), _f32(b)
     N, Cin, H, W = x.shape
     Cout, _, KH, KW = w.shape
-    Ho = (H + 2 * pad - dilation * (KH - 1) - 1) // stride + 1
-    Wo = (W + 2 * pad - dilation * (KW - 1) - 1) // stride + 1
+    (sh, sw), (ph, pw), (dh, dw) = _pair(stride), _pair(pad), _pair(dilation)
+    Ho = (H + 2 * ph - dh * (KH - 1) - 1) // sh + 1
+    Wo = (W + 2 * pw - dw * (KW - 1) - 1) // sw + 1
     out = np.empty((N, Cout, Ho, Wo), np.float32)
-    lib().naive_conv2d(_p(x), _p(w), _p(b), _p(out), N, Cin, H, W, Cout, KH, KW, stride, stride,
-                       pad, pad, dilation, dilation)
+    lib().naive_conv2d(_p(x), _p(w), _p(b), _p(out), N, Cin, H, W, Cout, KH, KW, sh, sw,
+                       ph, pw, dh, dw)
     return out
 
 

@@ -13,10 +13,12 @@ import torch
 import torch.nn.functional as F
 
 
-def conv2d(x, w, b=None, stride=1, pad=1):
-    """NCHW conv, zero padding.  Reference formula: src/kernels/conv2d.cu:88-164
-    (direct conv, fp32 accumulate) and src/kernels/conv2d.cuh:21-33."""
-    return F.conv2d(x, w, b, stride=stride, padding=pad)
+def conv2d(x, w, b=None, stride=1, pad=1, dilation=1):
+    """NCHW conv, zero padding; stride / pad / dilation an int or an (h, w)
+    pair.  Reference formula: src/kernels/conv2d.cu:88-164 (direct conv with
+    per-axis stride, padding and dilation, fp32 accumulate) and
+    src/kernels/conv2d.cuh:21-40."""
+    return F.conv2d(x, w, b, stride=stride, padding=pad, dilation=dilation)
 
 
 def gemm(a, b, c=None, alpha=1.0, beta=0.0, trans_a=False, trans_b=False):

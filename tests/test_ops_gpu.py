@@ -138,6 +138,28 @@ def test_conv2d_reference_api(gpu, N, Cin, H, W, Cout, k, s, p):
     assert_close(out, R.conv2d(x, w, b, s, p), "launch_conv2d")
 
 
+@pytest.mark.parametrize("N,Cin,H,W,Cout,KH,KW,sh,sw,ph,pw,dh,dw", [
+    (1, 320, 64, 64, 320, 3, 3, 1, 1, 2, 2, 2, 2),      # channel-aligned (LDS-DMA) path
+    (2, 128, 33, 31, 64, 3, 3, 2, 1, 3, 1, 3, 1),       # anisotropic, dilated
+    (2, 64, 17, 23, 96, 3, 5, 1, 2, 1, 4, 2, 2),        # KH != KW
+    (1, 4, 20, 18, 8, 3, 3, 2, 1, 1, 0, 1, 3),          # small-channel (generic loader) path
+    (2, 3, 9, 11, 5, 3, 3, 1, 1, 0, 0, 4, 4),           # dilation larger than the padding
+])
+def test_conv2d_reference_api_geometry(gpu, N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, dh, dw):
+    """Per-axis stride / pad and dilation of launch_conv2d (src/kernels/conv2d.cu:88-164)."""
+    announce(f"launch_conv2d geometry N={N} Cin={Cin} {H}x{W} Cout={Cout} k={KH}x{KW} "
+             f"s=({sh},{sw}) p=({ph},{pw}) d=({dh},{dw})")
+    x = randn((N, Cin, H, W), 33)
+    w = randn((Cout, Cin, KH, KW), 34, std=1.0 / math.sqrt(Cin * KH * KW))
+    b = randn((Cout,), 35, std=0.1)
+    Ho = (H + 2 * ph - dh * (KH - 1) - 1) // sh + 1
+    Wo = (W + 2 * pw - dw * (KW - 1) - 1) // sw + 1
+    out = torch.empty(N, Cout, Ho, Wo, dtype=torch.float16, device=gpu)
+    ops.launch_conv2d(to_gpu(x), to_gpu(w), to_gpu(b), out, N, Cin, H, W, Cout, KH, KW,
+                      sh, sw, ph, pw, dh, dw)
+    assert_close(out, R.conv2d(x, w, b, (sh, sw), (ph, pw), (dh, dw)), "launch_conv2d geometry")
+
+
 def test_conv_nhwc_concat_shortcut_residual_tbias(gpu):
     """ResnetBlock2D conv2 form: 3x3 over h, fused 1x1 shortcut over concat(x_a, x_b),
     per-(n,c) time bias."""

@@ -51,15 +51,29 @@ def _built():
 
 
 # ---------------------------------------------------------------- conv
-@pytest.mark.parametrize("stride,pad,dil,k", [(1, 1, 1, 3), (2, 1, 1, 3), (1, 0, 1, 1), (1, 2, 2, 3)])
+@pytest.mark.parametrize("stride,pad,dil,k", [(1, 1, 1, 3), (2, 1, 1, 3), (1, 0, 1, 1), (1, 2, 2, 3),
+                                             ((2, 1), (1, 0), (1, 3), 3), ((1, 2), (3, 2), (3, 2), 3)])
 def test_conv_torch_vs_c(stride, pad, dil, k):
     x, w, b = _rand((2, 5, 9, 7), 1), _rand((6, 5, k, k), 2, 0.2), _rand((6,), 3, 0.1)
     ref = torch.nn.functional.conv2d(x, w, b, stride=stride, padding=pad, dilation=dil)
     got = naive.conv2d(x, w, b, stride=stride, pad=pad, dilation=dil)
     assert got.shape == tuple(ref.shape)  # output-size formula, src/kernels/conv2d.cu:275-278
     _close(got, ref)
-    if dil == 1:
-        _close(R.conv2d(x, w, b, stride=stride, pad=pad), ref)
+    _close(R.conv2d(x, w, b, stride=stride, pad=pad, dilation=dil), ref)
+
+
+@pytest.mark.parametrize("dh,dw", [(2, 2), (3, 1), (1, 2)])
+def test_conv_dilation_is_zero_inserted_kernel(dh, dw):
+    """A conv with dilation (dh, dw) equals the undilated conv whose kernel has
+    (dh - 1, dw - 1) zero rows / columns inserted between taps
+    (src/kernels/conv2d.cu:88-164 reads input row oh*sh - ph + kh*dh)."""
+    x, w = _rand((2, 3, 11, 12), 4), _rand((4, 3, 3, 3), 5, 0.3)
+    wz = torch.zeros(4, 3, 2 * dh + 1, 2 * dw + 1)
+    wz[:, :, ::dh, ::dw] = w
+    for pad in ((1, 1), (2, 3)):
+        got = naive.conv2d(x, w, None, stride=1, pad=pad, dilation=(dh, dw))
+        ref = naive.conv2d(x, wz, None, stride=1, pad=pad, dilation=1)
+        _close(got, ref)
 
 
 def test_conv_delta_kernel_is_shifted_copy():
