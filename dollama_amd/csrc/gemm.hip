@@ -1136,6 +1136,14 @@ static const SplitWorkspace* split_workspace(hipStream_t s) {
 // thread that set them.
 static thread_local int g_forced_split = 0;
 static thread_local int g_variant = 0;  // bits select alternative heuristics
+// Set while an allocation-free entry point runs: split-K stays off, since its
+// workspace is allocated on first use.
+static thread_local bool t_no_split = false;
+struct NoSplitScope {
+  bool prev;
+  NoSplitScope() : prev(t_no_split) { t_no_split = true; }
+  ~NoSplitScope() { t_no_split = prev; }
+};
 
 template <int BM, int BN, int WM, int WN, int NS, bool PF = false, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
@@ -1146,6 +1154,7 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   const int tiles = tiles_m * tiles_n;
   const int nk = (bd.K + BK - 1) / BK;
   if (g_forced_split > 0) S = g_forced_split;
+  if (t_no_split) S = 1;
   SplitArgs sp{1, nk, nullptr, nullptr};
   if (S > 1 && nk > 1) {
     const int kps = (nk + S - 1) / S;
@@ -1889,6 +1898,34 @@ static int conv2d_nchw_check(const void* in, const void* weight, void* out, int 
 
 }  // namespace dlm
 
+// The allocation-free conv's staging memory: one array per GPU, resolved to
+// a device address with hipGetSymbolAddress once per device (the array's
+// name is only a host-side stand-in in host code).
+constexpr size_t kNoAllocScratchBytes = DLM_CONV2D_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace dlm {
+namespace {
+std::mutex g_noalloc_mu;
+std::vector<void*> g_noalloc_ptr;  // [device] -> device address of `scratch`
+
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  DLM_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if ((int)g_noalloc_ptr.size() <= dev) g_noalloc_ptr.resize(dev + 1, nullptr);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    DLM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(DLM_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+    g_noalloc_ptr[dev] = p;
+  }
+  *out = g_noalloc_ptr[dev];
+  return DLM_OK;
+}
+}  // namespace
+}  // namespace dlm
+
 extern "C" {
 
 int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out, int N,
@@ -1906,6 +1943,29 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
   f16* wp = (f16*)scratch_slot(wb, 3, s, &st);
   if (!wp) return st;
   return conv2d_nchw_run(in, weight, bias, out, N, Cin, H, W, Cout, KH, KW, g, x, wp, s);
+}
+
+int dlm_conv2d_fp16_noalloc(const void* in, const void* weight, const void* bias, void* out,
+                            int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride_h,
+                            int stride_w, int pad_h, int pad_w, int dilation_h, int dilation_w,
+                            void* stream) {
+  const ConvGeom g{stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w};
+  bool noop = true;
+  int st = conv2d_nchw_check(in, weight, out, N, Cin, H, W, Cout, KH, KW, g, &noop);
+  if (st != DLM_OK || noop) return st;
+  size_t xb = 0, wb = 0;
+  conv2d_nchw_staging(N, Cin, H, W, Cout, KH, KW, &xb, &wb);
+  const size_t x_off = 0, w_off = (xb + 255) & ~size_t(255);
+  if (w_off + wb > kNoAllocScratchBytes)
+    return fail(DLM_ERR_INVALID_ARG,
+                "dlm_conv2d_fp16_noalloc: staging needs " + std::to_string(w_off + wb) +
+                    " bytes, above the fixed maximum of " + std::to_string(kNoAllocScratchBytes));
+  void* base = nullptr;
+  if ((st = noalloc_scratch(&base)) != DLM_OK) return st;
+  unsigned char* b = (unsigned char*)base;
+  NoSplitScope no_split;  // split-K would need the lazily allocated workspace
+  return conv2d_nchw_run(in, weight, bias, out, N, Cin, H, W, Cout, KH, KW, g, (f16*)(b + x_off),
+                         (f16*)(b + w_off), (hipStream_t)stream);
 }
 
 }  // extern "C"

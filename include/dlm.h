@@ -102,6 +102,24 @@ int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* 
                     int stride_h, int stride_w, int pad_h, int pad_w,
                     int dilation_h, int dilation_w, void* stream);
 
+/* Allocation-free variant of dlm_conv2d_fp16 (same arguments, same kernels,
+ * bit-identical output).  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The staging (channels-
+ * last input padded to a multiple of 8 channels, then the packed weight at
+ * the next 256-byte boundary: 2*N*H*W*Cin8 + 2*Cout*KH*KW*Cin8 bytes) lives
+ * in one fixed array of DLM_CONV2D_NOALLOC_MAX_BYTES per GPU, held from the
+ * library's first use of that GPU until the process ends; a call needing
+ * more returns DLM_ERR_INVALID_ARG before launching anything.  Split-K is
+ * not used.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two threads) race and must be ordered by
+ * the caller. */
+#define DLM_CONV2D_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int dlm_conv2d_fp16_noalloc(const void* in, const void* weight, const void* bias, void* out,
+                            int N, int Cin, int H, int W, int Cout, int KH, int KW,
+                            int stride_h, int stride_w, int pad_h, int pad_w,
+                            int dilation_h, int dilation_w, void* stream);
+
 /* C = alpha * op(A) op(B) + beta * C, row-major, fp16 in/out, fp32 accumulate.
  * op(A) = [M,K], op(B) = [K,N].
  * Replaces dollama::launch_gemm_fp16 (src/kernels/gemm.cuh:44-53). */
