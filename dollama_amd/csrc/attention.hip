@@ -234,6 +234,7 @@ struct FlashVtParams {
   int Sq, Sk;
   float c;                  // scale * log2(e)
   unsigned k_bytes, vt_bytes;
+  int nqb, H, B;            // query blocks per head, heads, batch: the 1-D grid's shape
 };
 
 __device__ __forceinline__ i32x4 fa_rsrc(const void* p, unsigned bytes) {
@@ -288,11 +289,25 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   constexpr int DI = 8 / NWV;  // DMA instructions per wave per operand tile
   __shared__ __attribute__((aligned(1024))) unsigned char smem_g[FA_NS * FA_STAGE];
   unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_g;
-  const int b = blockIdx.z, h = blockIdx.y;
+  // XCD-aware placement: the hardware deals workgroup i to XCD i % 8 and each
+  // XCD has its own L2, so consecutive logical blocks (the query blocks of one
+  // head, then the next head) are given to one XCD; each L2 then fetches the
+  // K / V^T of its own heads only.
+  int b, h, qb;
+  {
+    const int total = p.nqb * p.H * p.B;
+    const int q8 = total >> 3, r8 = total & 7;
+    const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int logical = x * q8 + (x < r8 ? x : r8) + slot;
+    qb = logical % p.nqb;
+    const int bh = logical / p.nqb;
+    h = bh % p.H;
+    b = bh / p.H;
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;
-  const int q0 = blockIdx.x * (NWV * 32) + wave * 32;
+  const int q0 = qb * (NWV * 32) + wave * 32;
 
   f16x8 qf[4];
   {
@@ -501,12 +516,14 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   // 64-query workgroups: twice the K/V staging, but waves spread evenly.
   // Cross attention (every key in at most two tiles): always 128-query
   // workgroups, whose one K/V staging serves twice the queries.
+  p.H = a->H;
+  p.B = a->B;
   if (a->Sk > 2 * FA_TK && (long long)((a->Sq + 127) / 128) * a->H * a->B < 512) {
-    const dim3 grid((a->Sq + 63) / 64, a->H, a->B);
-    hipLaunchKernelGGL(flash_vt_pipe_kernel<2>, grid, dim3(128), 0, s, p);
+    p.nqb = (a->Sq + 63) / 64;
+    hipLaunchKernelGGL(flash_vt_pipe_kernel<2>, dim3(p.nqb * p.H * p.B), dim3(128), 0, s, p);
   } else {
-    const dim3 grid((a->Sq + 127) / 128, a->H, a->B);
-    hipLaunchKernelGGL(flash_vt_pipe_kernel<4>, grid, dim3(256), 0, s, p);
+    p.nqb = (a->Sq + 127) / 128;
+    hipLaunchKernelGGL(flash_vt_pipe_kernel<4>, dim3(p.nqb * p.H * p.B), dim3(256), 0, s, p);
   }
   DLM_LAUNCH_CHECK();
   return DLM_OK;
