@@ -19,6 +19,7 @@
 //     is also lane-per-query and the online-softmax rescale is per lane.
 // Q, K, V and O are addressed with independent batch / token / head strides,
 // so the fused QKV projection output [B, S, 3C] is read in place.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -585,14 +586,28 @@ __device__ __forceinline__ void block_max_sum(float& m, float& l, float* red) {
   }
 }
 
+// Row softmax of `cols` scores (any count; lds a multiple of 4 and at least
+// cols rounded up to 4) into fp16 P, writing colw (a multiple of 4, >= cols)
+// columns: probabilities for [0, cols), zeros for [cols, colw).
+__device__ __forceinline__ float4 mask4(float4 x, int v, int cols) {
+  const int c = 4 * v;
+  if (c + 0 >= cols) x.x = -INFINITY;
+  if (c + 1 >= cols) x.y = -INFINITY;
+  if (c + 2 >= cols) x.z = -INFINITY;
+  if (c + 3 >= cols) x.w = -INFINITY;
+  return x;
+}
+
 template <int VPT>
 __global__ void __launch_bounds__(256)
 softmax_rows_kernel(const float* __restrict__ S, long long lds, f16* __restrict__ P, long long ldp,
-                    int cols) {
+                    int cols, int colw) {
   __shared__ float red[8];
   const float* row = S + (size_t)blockIdx.x * lds;
   f16* prow = P + (size_t)blockIdx.x * ldp;
-  const int nv = cols >> 2;
+  const int nv = (cols + 3) >> 2;  // vectors holding scores
+  const int nw = colw >> 2;        // vectors written
+  const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
   const int t = threadIdx.x;
   float m = -INFINITY, l = 0.0f;
   if (VPT > 0) {
@@ -600,8 +615,7 @@ softmax_rows_kernel(const float* __restrict__ S, long long lds, f16* __restrict_
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int v = t + i * 256;
-      x[i] = v < nv ? reinterpret_cast<const float4*>(row)[v]
-                    : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      x[i] = v < nv ? mask4(reinterpret_cast<const float4*>(row)[v], v, cols) : ninf;
       m = fmaxf(m, fmaxf(fmaxf(x[i].x, x[i].y), fmaxf(x[i].z, x[i].w)));
     }
     if (m != -INFINITY) {
@@ -614,7 +628,7 @@ softmax_rows_kernel(const float* __restrict__ S, long long lds, f16* __restrict_
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int v = t + i * 256;
-      if (v < nv) {
+      if (v < nw) {
         const f16x4 o = {(f16)(__expf(x[i].x - m) * inv), (f16)(__expf(x[i].y - m) * inv),
                          (f16)(__expf(x[i].z - m) * inv), (f16)(__expf(x[i].w - m) * inv)};
         *reinterpret_cast<f16x4*>(prow + 4 * v) = o;
@@ -622,22 +636,157 @@ softmax_rows_kernel(const float* __restrict__ S, long long lds, f16* __restrict_
     }
   } else {
     for (int v = t; v < nv; v += 256) {
-      const float4 x = reinterpret_cast<const float4*>(row)[v];
+      const float4 x = mask4(reinterpret_cast<const float4*>(row)[v], v, cols);
       const float mx = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
       const float mn = fmaxf(m, mx);
-      l = l * __expf(m - mn) + __expf(x.x - mn) + __expf(x.y - mn) + __expf(x.z - mn) +
-          __expf(x.w - mn);
+      l = (mn == -INFINITY) ? 0.0f
+                            : l * __expf(m - mn) + __expf(x.x - mn) + __expf(x.y - mn) +
+                                  __expf(x.z - mn) + __expf(x.w - mn);
       m = mn;
     }
     block_max_sum(m, l, red);
     const float inv = 1.0f / l;
-    for (int v = t; v < nv; v += 256) {
-      const float4 x = reinterpret_cast<const float4*>(row)[v];
+    for (int v = t; v < nw; v += 256) {
+      const float4 x = v < nv ? mask4(reinterpret_cast<const float4*>(row)[v], v, cols) : ninf;
       const f16x4 o = {(f16)(__expf(x.x - m) * inv), (f16)(__expf(x.y - m) * inv),
                        (f16)(__expf(x.z - m) * inv), (f16)(__expf(x.w - m) * inv)};
       *reinterpret_cast<f16x4*>(prow + 4 * v) = o;
     }
   }
+}
+
+int softmax_rows(const float* S, long long lds, f16* P, long long ldp, int rows, int cols, int colw,
+                 hipStream_t s) {
+  if (colw <= 256 * 4 * 4)
+    hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
+  else if (colw <= 256 * 4 * 16)
+    hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
+  else
+    hipLaunchKernelGGL(softmax_rows_kernel<0>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Reference-layout attention ([B, H, S, Dh] Q / K / V / O, any Dh), the
+// counterpart of the reference's launch_attention dispatch
+// (src/kernels/attention.cu:602-700: flash kernels up to its shared-memory
+// limit, a one-row-per-block kernel beyond).
+//   Dh == 64: V is transposed per head (zero-padded to a multiple of 8 keys)
+//   and the pipelined flash kernel runs;
+//   any other Dh: per head, fp32 scores = scale Q K^T (MFMA GEMM), row
+//   softmax to fp16 P, O = P V (MFMA GEMM over V^T), query rows in chunks so
+//   the scores of one chunk stay within 256 MiB.  Q / K rows are copied to a
+//   pitch padded to a multiple of 8 (zeros) when Dh is not one or the bases
+//   are not 16-byte aligned.
+// ---------------------------------------------------------------------------
+// out[r * ld + c] = c < cols ? in[r * cols + c] : 0
+__global__ void pad_rows_kernel(const f16* __restrict__ in, f16* __restrict__ out, long long rows,
+                                int cols, int ld) {
+  const long long total = rows * ld;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long r = i / ld;
+    const int c = (int)(i - r * ld);
+    out[i] = c < cols ? in[r * cols + c] : (f16)0.0f;
+  }
+}
+
+// Per head z: out[z][d][key] = v[z][key][d] for key < Sk, 0 for key in [Sk, ld).
+__global__ void vt_pad_kernel(const f16* __restrict__ v, f16* __restrict__ out, int Sk, int Dh,
+                              int ld) {
+  __shared__ f16 tile[32][33];
+  const long long z = blockIdx.z;
+  const int k0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
+  const int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
+  const f16* src = v + z * Sk * (long long)Dh;
+  for (int r = ty; r < 32; r += 8) {
+    const int key = k0 + r, d = d0 + tx;
+    tile[r][tx] = (key < Sk && d < Dh) ? src[(long long)key * Dh + d] : (f16)0.0f;
+  }
+  __syncthreads();
+  f16* dst = out + z * Dh * (long long)ld;
+  for (int r = ty; r < 32; r += 8) {
+    const int d = d0 + r, key = k0 + tx;
+    if (d < Dh && key < ld) dst[(long long)d * ld + key] = tile[tx][r];
+  }
+}
+
+static int vt_pad(const f16* v, f16* out, long long BH, int Sk, int Dh, int ld, hipStream_t s) {
+  const dim3 grid((ld + 31) / 32, (Dh + 31) / 32, (unsigned)BH);
+  hipLaunchKernelGGL(vt_pad_kernel, grid, dim3(32, 8), 0, s, v, out, Sk, Dh, ld);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+static int pad_rows(const f16* in, f16* out, long long rows, int cols, int ld, hipStream_t s) {
+  const long long total = rows * ld;
+  const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, s, in, out, rows, cols, ld);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+static int attention_reference_layout(const f16* q, const f16* k, const f16* v, f16* o, int B,
+                                      int H, int Sq, int Sk, int Dh, float scale, hipStream_t s) {
+  const long long BH = (long long)B * H;
+  const int K8 = (Sk + 7) & ~7;
+  int st = DLM_OK;
+  if (Dh == 64 && dlm_aligned16(q) && dlm_aligned16(k) && ((uintptr_t)o & 7) == 0) {
+    f16* vt = (f16*)scratch_slot((size_t)BH * 64 * K8 * 2, 6, s, &st);
+    if (!vt) return st;
+    if ((st = vt_pad(v, vt, BH, Sk, 64, K8, s)) != DLM_OK) return st;
+    dlm_attention_vt_args a{};
+    a.q = q; a.k = k; a.vt = vt; a.o = o;
+    a.q_sh = (long long)Sq * 64; a.q_sb = a.q_sh * H; a.q_ss = 64;
+    a.k_sh = (long long)Sk * 64; a.k_sb = a.k_sh * H; a.k_ss = 64;
+    a.vt_sh = 64LL * K8; a.vt_sb = a.vt_sh * H; a.vt_ld = K8;
+    a.o_sh = (long long)Sq * 64; a.o_sb = a.o_sh * H; a.o_ss = 64;
+    a.B = B; a.H = H; a.Sq = Sq; a.Sk = Sk; a.scale = scale;
+    a.k_bytes = (unsigned long long)BH * Sk * 64 * 2;
+    a.vt_bytes = (unsigned long long)BH * 64 * K8 * 2;
+    if (a.k_bytes >= (1ull << 31) || a.vt_bytes >= (1ull << 31))
+      return fail(DLM_ERR_UNSUPPORTED, "attention: K or V larger than 2 GiB");
+    return attention_vt(&a, s);
+  }
+  const int D8 = (Dh + 7) & ~7;
+  const int K4 = (Sk + 3) & ~3;
+  const f16* qp = q;
+  const f16* kp = k;
+  int ld = Dh;
+  if (Dh % 8 != 0 || !dlm_aligned16(q) || !dlm_aligned16(k)) {
+    f16* qb = (f16*)scratch_slot((size_t)BH * Sq * D8 * 2, 7, s, &st);
+    if (!qb) return st;
+    f16* kb = (f16*)scratch_slot((size_t)BH * Sk * D8 * 2, 8, s, &st);
+    if (!kb) return st;
+    if ((st = pad_rows(q, qb, BH * Sq, Dh, D8, s)) != DLM_OK) return st;
+    if ((st = pad_rows(k, kb, BH * Sk, Dh, D8, s)) != DLM_OK) return st;
+    qp = qb;
+    kp = kb;
+    ld = D8;
+  }
+  f16* vt = (f16*)scratch_slot((size_t)BH * Dh * K8 * 2, 6, s, &st);
+  if (!vt) return st;
+  if ((st = vt_pad(v, vt, BH, Sk, Dh, K8, s)) != DLM_OK) return st;
+  const long long rows_cap = std::max<long long>(1, (256LL << 20) / (4LL * K4));
+  const int rows = (int)std::min<long long>(Sq, rows_cap);
+  float* S = (float*)scratch_slot((size_t)rows * K4 * 4, 9, s, &st);
+  if (!S) return st;
+  f16* P = (f16*)scratch_slot((size_t)rows * K8 * 2, 10, s, &st);
+  if (!P) return st;
+  for (long long z = 0; z < BH; ++z) {
+    for (int r0 = 0; r0 < Sq; r0 += rows) {
+      const int n = std::min(rows, Sq - r0);
+      st = dlm_linear_f32out_fp16(qp + (z * Sq + r0) * ld, ld, kp + z * Sk * ld, ld, nullptr,
+                                  nullptr, 0, S, K4, n, Sk, ld, scale, 0.0f, DLM_ACT_NONE, s);
+      if (st != DLM_OK) return st;
+      if ((st = softmax_rows(S, K4, P, K8, n, Sk, K8, s)) != DLM_OK) return st;
+      st = dlm_linear_fp16(P, K8, vt + z * Dh * (long long)K8, K8, nullptr, nullptr, 0,
+                           o + (z * Sq + r0) * Dh, Dh, n, Dh, K8, 1.0f, 0.0f, DLM_ACT_NONE, s);
+      if (st != DLM_OK) return st;
+    }
+  }
+  return DLM_OK;
 }
 
 }  // namespace dlm
@@ -695,30 +844,18 @@ int dlm_softmax_rows_f32_fp16(const float* S, long long lds, void* P, long long 
   DLM_REQUIRE(cols % 4 == 0 && lds % 4 == 0 && ldp % 4 == 0 && lds >= cols && ldp >= cols,
               "cols, lds and ldp must be multiples of 4 with lds, ldp >= cols");
   DLM_REQUIRE(dlm_aligned16(S) && ((uintptr_t)P & 7) == 0, "S must be 16-byte, P 8-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  if (cols <= 256 * 4 * 4)
-    hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(rows), dim3(256), 0, s, S, lds, (f16*)P, ldp, cols);
-  else if (cols <= 256 * 4 * 16)
-    hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(rows), dim3(256), 0, s, S, lds, (f16*)P, ldp,
-                       cols);
-  else
-    hipLaunchKernelGGL(softmax_rows_kernel<0>, dim3(rows), dim3(256), 0, s, S, lds, (f16*)P, ldp,
-                       cols);
-  DLM_LAUNCH_CHECK();
-  return DLM_OK;
+  return softmax_rows(S, lds, (f16*)P, ldp, rows, cols, cols, (hipStream_t)stream);
 }
 
 int dlm_attention_fp16(const void* q, const void* k, const void* v, void* out, int B, int H,
                        int Sq, int Sk, int Dh, float scale, void* stream) {
   if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || Dh <= 0) return DLM_OK;
-  dlm_attention_args a{};
-  a.q = q; a.k = k; a.v = v; a.o = out;
-  a.q_sh = (long long)Sq * Dh; a.q_sb = a.q_sh * H; a.q_ss = Dh;
-  a.k_sh = (long long)Sk * Dh; a.k_sb = a.k_sh * H; a.k_ss = Dh;
-  a.v_sh = (long long)Sk * Dh; a.v_sb = a.v_sh * H; a.v_ss = Dh;
-  a.o_sh = (long long)Sq * Dh; a.o_sb = a.o_sh * H; a.o_ss = Dh;
-  a.B = B; a.H = H; a.Sq = Sq; a.Sk = Sk; a.Dh = Dh; a.scale = scale;
-  return dlm_attention_strided_fp16(&a, stream);
+  DLM_REQUIRE(q && k && v && out, "NULL operand");
+  const long long BH = (long long)B * H;
+  DLM_REQUIRE(BH * std::max(Sq, Sk) * (long long)((Dh + 7) & ~7) * 2 < (1LL << 31),
+              "Q, K or V larger than 2 GiB");
+  return attention_reference_layout((const f16*)q, (const f16*)k, (const f16*)v, (f16*)out, B, H,
+                                    Sq, Sk, Dh, scale, (hipStream_t)stream);
 }
 
 }  // extern "C"

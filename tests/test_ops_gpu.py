@@ -282,6 +282,37 @@ def test_attention_reference_api(gpu, B, H, Sq, Sk):
     assert_close(out, ref, "attention")
 
 
+@pytest.mark.parametrize("B,H,Sq,Sk,Dh", [(1, 2, 100, 33, 40), (2, 3, 257, 77, 80), (1, 1, 1024, 1024, 512),
+                                          (2, 2, 65, 129, 20), (1, 3, 48, 5, 128), (2, 1, 96, 96, 8),
+                                          (1, 1, 300, 1, 36)])
+def test_attention_reference_api_any_head_dim(gpu, B, H, Sq, Sk, Dh):
+    """launch_attention for head dims other than 64 (src/kernels/attention.cu:602-700 accepts
+    any Dh; the VAE mid block uses Dh = 512): odd key counts, Dh not a multiple of 8, Sk = 1."""
+    announce(f"launch_attention B={B} H={H} Sq={Sq} Sk={Sk} Dh={Dh}")
+    q, k, v = randn((B, H, Sq, Dh), 103), randn((B, H, Sk, Dh), 104), randn((B, H, Sk, Dh), 105)
+    scale = 1.0 / math.sqrt(Dh)
+    out = torch.empty(B, H, Sq, Dh, dtype=torch.float16, device=gpu)
+    ops.launch_attention(to_gpu(q), to_gpu(k), to_gpu(v), out, B, H, Sq, Sk, Dh, scale)
+    ref = torch.cat([R.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], scale) for b in range(B)])
+    assert_close(out, ref, f"attention Dh={Dh}")
+
+
+def test_attention_reference_api_unaligned(gpu):
+    """Q / K / V / O that start 2 bytes into their allocation take the general path."""
+    B, H, Sq, Sk, Dh = 1, 2, 70, 45, 64
+    announce("launch_attention unaligned operands")
+    q, k, v = randn((B, H, Sq, Dh), 106), randn((B, H, Sk, Dh), 107), randn((B, H, Sk, Dh), 108)
+    def shifted(t):
+        buf = torch.zeros(t.numel() + 1, dtype=torch.float16, device=gpu)
+        buf[1:] = t.reshape(-1).to(torch.float16)
+        return buf[1:]
+    out_buf = torch.zeros(B * H * Sq * Dh + 1, dtype=torch.float16, device=gpu)
+    out = out_buf[1:]
+    ops.launch_attention(shifted(q), shifted(k), shifted(v), out, B, H, Sq, Sk, Dh, 0.125)
+    ref = R.attention(q, k, v, 0.125)
+    assert_close(out.reshape(B, H, Sq, Dh), ref, "attention unaligned")
+
+
 def test_attention_strided_fused_qkv(gpu):
     """Q/K/V read in place from a fused [B, S, 3C] projection, O written to [B, S, C]."""
     B, S, Hh, Dh = 2, 256, 4, 64
