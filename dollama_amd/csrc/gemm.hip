@@ -1039,8 +1039,10 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
     DLM_WAIT_VM(0);  // this wave's partial is complete at agent scope
     __syncthreads();  // every wave's partial complete, every fragment read done
     int* flag = reinterpret_cast<int*>(smem_generic);  // the operand ring is free now
+    // acquire-release at agent scope: this split's partial (and every earlier
+    // split's, through the counter) happens-before the last split's reads
     if (tid == 0)
-      *flag = __hip_atomic_fetch_add(sp.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = __hip_atomic_fetch_add(sp.cnt + tile, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (*flag != sp.S - 1) return;
     f32x4 tot[TM][TN];

@@ -644,4 +644,8 @@ int dlm_arena_reserve(int id, size_t bytes) {
   return guarded([&] { device_arena_reserve(arena_id(id), bytes); });
 }
 
+int dlm_arena_fill(int id, int pattern) {
+  return guarded([&] { device_arena_fill(arena_id(id), pattern); });
+}
+
 }  // extern "C"

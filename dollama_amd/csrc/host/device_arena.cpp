@@ -183,9 +183,11 @@ void device_arena_reserve(DeviceArenaId id, size_t bytes) {
   Arena& a = arena(id);
   std::lock_guard<std::mutex> lock(a.mu);
   claim(a, id);
+  // with the pool off there are no chunks to replace: a no-op, as in the
+  // reference (device_arena.cu reserve under DOLLAMA_POOL=0)
+  if (!device_arena_pool_enabled()) return;
   if (live(a)) throw std::runtime_error("device_arena_reserve: arena is not quiescent");
   a.reserved = bytes;
-  if (!device_arena_pool_enabled()) return;
   if (!a.chunks.empty() && a.chunks.front().bytes >= bytes) return;
   for (Chunk& c : a.chunks) {
     DLM_CALL(dlm_free(c.ptr));
@@ -224,6 +226,15 @@ void device_arena_release(DeviceArenaId id) {
   a.st.live_chunks = 0;
   a.st.bytes_in_use = 0;
   a.st.reserved_bytes = 0;
+}
+
+void device_arena_fill(DeviceArenaId id, int pattern) {
+  Arena& a = arena(id);
+  std::lock_guard<std::mutex> lock(a.mu);
+  claim(a, id);
+  if (live(a)) throw std::runtime_error("device_arena_fill: arena is not quiescent");
+  for (const Chunk& c : a.chunks) DLM_CALL(dlm_memset_async(c.ptr, pattern & 0xFF, c.bytes, nullptr));
+  DLM_CALL(dlm_device_synchronize());
 }
 
 bool device_arena_release_noexcept(DeviceArenaId id) noexcept {

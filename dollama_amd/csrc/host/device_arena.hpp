@@ -59,6 +59,11 @@ bool device_arena_release_noexcept(DeviceArenaId id) noexcept;
 DeviceArenaStats device_arena_stats(DeviceArenaId id);
 void device_arena_reset_counters(DeviceArenaId id);
 size_t device_arena_first_chunk_bytes(DeviceArenaId id);
+// Fill every byte the arena holds (all chunks) with `pattern`, synchronously;
+// throws std::runtime_error while allocations are live.  A determinism check:
+// scratch that a computation reads before writing shows up as a changed
+// result after the arena was filled with different patterns.
+void device_arena_fill(DeviceArenaId id, int pattern);
 // Changes whenever the arena's chunk list changes (new chunk, reserve,
 // release): equal epoch and equal mark mean that the same sequence of
 // allocations returns the same addresses (used to reuse captured graphs).

@@ -210,13 +210,19 @@ void SafeTensors::parse_header(const std::string& json) {
       j.expect('}');
       if (!have_dtype || !have_shape || !have_off) j.fail("tensor entry missing a field");
       if (e.end > data_bytes_) throw std::runtime_error("safetensors: tensor '" + key + "' beyond file end");
+      // element count and byte size with overflow checks: a crafted header
+      // must not wrap n * es around to the stored byte range
       size_t n = 1;
       for (int64_t d : e.shape) {
         if (d < 0) j.fail("negative dimension");
-        n *= (size_t)d;
+        if (__builtin_mul_overflow(n, (size_t)d, &n))
+          throw std::runtime_error("safetensors: tensor '" + key + "' shape overflows");
       }
       const size_t es = dtype_size(e.dtype);
-      if (es != 0 && n * es != e.end - e.begin)
+      size_t nbytes = 0;
+      if (es != 0 && __builtin_mul_overflow(n, es, &nbytes))
+        throw std::runtime_error("safetensors: tensor '" + key + "' byte size overflows");
+      if (es != 0 && nbytes != e.end - e.begin)
         throw std::runtime_error("safetensors: tensor '" + key + "' size does not match shape");
       entries_[key] = e;
       names_.push_back(key);

@@ -727,7 +727,10 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
   void* h = sc.alloc<uint16_t>((size_t)M * C);
   void* n = sc.alloc<uint16_t>((size_t)M * C);
   void* qkv = sc.alloc<uint16_t>((size_t)M * 2 * C);
-  void* vt = sc.alloc<uint16_t>((size_t)M * C);
+  // V^T rows are padded to a multiple of 8 tokens (the attention kernel's
+  // key granularity); the QKV epilogue writes zeros into the padding
+  const int vt_ld = (HW + 7) & ~7;
+  void* vt = sc.alloc<uint16_t>((size_t)B * C * vt_ld);
   void* o = sc.alloc<uint16_t>((size_t)M * C);
   void* f = sc.alloc<uint16_t>((size_t)M * 4 * C);
   const float scale = 1.0f / std::sqrt(64.0f);
@@ -741,8 +744,8 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
     LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
     // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
     LAUNCH(kLinear, 2.0 * M * 3 * C * C, 0.0,
-           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, HW, M, 3 * C,
-                              C, stream));
+           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, vt_ld, M,
+                              3 * C, C, stream));
     {
       dlm_attention_vt_args a{};
       const char* base = static_cast<const char*>(qkv);
@@ -752,9 +755,9 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
       a.q_sb = a.k_sb = (long long)HW * 2 * C;
       a.q_ss = a.k_ss = 2 * C;
       a.q_sh = a.k_sh = 64;
-      a.vt_sb = (long long)C * HW;
-      a.vt_sh = 64LL * HW;
-      a.vt_ld = HW;
+      a.vt_sb = (long long)C * vt_ld;
+      a.vt_sh = 64LL * vt_ld;
+      a.vt_ld = vt_ld;
       a.o = o;
       a.o_sb = (long long)HW * C;
       a.o_ss = C;
@@ -765,7 +768,7 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
       a.Sk = HW;
       a.scale = scale;
       a.k_bytes = ((size_t)M * 2 * C - C) * kH;
-      a.vt_bytes = (size_t)M * C * kH;
+      a.vt_bytes = (size_t)B * C * vt_ld * kH;
       LAUNCH(kAttention, 4.0 * B * heads * (double)HW * HW * 64, 0.0,
              dlm_attention_vt_fp16(&a, stream));
     }

@@ -74,6 +74,7 @@ HOST_SIGNATURES = {
     "dlm_unet_read_weight": (I, [P, ctypes.c_char_p, P, c_size_t, P]),
     "dlm_f32_to_f16": (I, [P, P, c_size_t]),
     "dlm_arena_stats": (I, [I, POINTER(c_uint64)]),
+    "dlm_arena_fill": (I, [I, I]),
     "dlm_arena_release": (I, [I]),
     "dlm_arena_reserve": (I, [I, c_size_t]),
 }
@@ -158,6 +159,11 @@ def arena_stats(arena_id: int) -> dict:
     v = (c_uint64 * 11)()
     _call("dlm_arena_stats", arena_id, v)
     return dict(zip(ARENA_STAT_FIELDS, list(v)))
+
+
+def arena_fill(arena_id: int, pattern: int) -> None:
+    """Fill every byte the (quiescent) arena holds with `pattern`."""
+    _call("dlm_arena_fill", arena_id, pattern)
 
 
 def _stream():

@@ -289,6 +289,12 @@ int dlm_st_read(void* handle, const char* name, void* out, size_t bytes);
 int dlm_arena_stats(int arena_id, uint64_t* out /* [11] */);
 int dlm_arena_release(int arena_id);
 int dlm_arena_reserve(int arena_id, size_t bytes);
+/* Fill all memory the arena holds with the byte `pattern` (synchronous);
+ * DLM_ERR_STATE-class failure while allocations are live.  Test support for
+ * the reference's poisoned-arena determinism gate
+ * (src/tests/test_unet_fast.cu:136-172): a forward that reads scratch before
+ * writing it gives different results after fills with different patterns. */
+int dlm_arena_fill(int arena_id, int pattern);
 
 #ifdef __cplusplus
 }

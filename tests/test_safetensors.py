@@ -101,3 +101,23 @@ def test_errors(lib, tmp_path):
     nb = ctypes.c_size_t()
     assert lib.dlm_st_info(h, b"__nope__", ctypes.byref(dt), ctypes.byref(nd), shp, ctypes.byref(nb)) == 5
     _lib.check(lib.dlm_st_close(h))
+
+
+def test_shape_whose_byte_size_wraps_is_rejected(lib, tmp_path):
+    """A header whose element count times the element size wraps around 2^64
+    to the stored byte range must be refused, not reported as that shape."""
+    import json
+    d2 = (2 ** 63 + 4) // 3            # 3 * d2 = 2^63 + 4; * 2 bytes = 2^64 + 8 -> 8 mod 2^64
+    assert 3 * d2 == 2 ** 63 + 4
+    hdr = json.dumps({"t": {"dtype": "F16", "shape": [3, d2], "data_offsets": [0, 8]}}).encode()
+    path = tmp_path / "wrap.safetensors"
+    path.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 8)
+    h = P()
+    assert lib.dlm_st_open(str(path).encode(), ctypes.byref(h)) != 0
+    assert "overflow" in _lib.last_error()
+    # the same file with an honest shape opens
+    hdr = json.dumps({"t": {"dtype": "F16", "shape": [2, 2], "data_offsets": [0, 8]}}).encode()
+    path.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 8)
+    h = _open(lib, str(path))
+    assert _info(lib, h, "t")[:2] == (F16, (2, 2))
+    _lib.check(lib.dlm_st_close(h))

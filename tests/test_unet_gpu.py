@@ -146,3 +146,19 @@ def test_unet_sdxl_full_parity(gpu):
     s = metrics.ssim_uniform(out, ref)
     print(f"[parity] sdxl noise_pred SSIM={s:.7f}", flush=True)
     assert s >= 0.99999
+
+
+@pytest.mark.parametrize("H,W", [(24, 24), (40, 12)])
+def test_unet_tiny_parity_other_latent_sizes(gpu, H, W):
+    """Latents whose lower levels hold token counts that are not multiples of 8
+    (24x24: 576 / 144 / 36 tokens; 40x12: 480 / 120 / 30)."""
+    cfg = TINY
+    B, L = 2, 77
+    print(f"[case] tiny UNet B={B} {H}x{W} L={L}", flush=True)
+    Wc = OR.random_weights(OR.TINY, seed=17)
+    lat, ts, ehs, text, ids = _inputs(cfg, B, H, W, L, seed=18)
+    ref = OR.unet_forward(Wc, OR.TINY, lat, ts, ehs, text, ids)
+    net, out = _run_gpu(cfg, _to_gpu(Wc), lat, ts, ehs, text, ids)
+    assert out.shape == ref.shape
+    assert_close(out, ref, f"tiny noise_pred {H}x{W}")
+    net.close()
