@@ -246,6 +246,22 @@ int dlm_unet_forward(void* handle, int B, int H, int W, const void* latent, cons
   });
 }
 
+int dlm_unet_run_resnet(void* handle, const char* prefix, const void* xa, int Ca, const void* xb,
+                        int Cb, void* out, int B, int H, int W, const void* temb, void* stream) {
+  return guarded([&] {
+    if (!handle || !prefix) throw std::invalid_argument("NULL argument");
+    static_cast<UNet*>(handle)->run_resnet(prefix, xa, Ca, xb, Cb, out, B, H, W, temb, stream);
+  });
+}
+
+int dlm_unet_run_transformer_block(void* handle, const char* prefix, void* x, int B, int HW,
+                                   const void* ehs, int ctx_len, void* stream) {
+  return guarded([&] {
+    if (!handle || !prefix) throw std::invalid_argument("NULL argument");
+    static_cast<UNet*>(handle)->run_transformer_block(prefix, x, B, HW, ehs, ctx_len, stream);
+  });
+}
+
 int dlm_unet_set_stage_hook(void* handle, dlm_unet_stage_hook hook, void* user) {
   return guarded([&] {
     if (!handle) throw std::invalid_argument("NULL handle");

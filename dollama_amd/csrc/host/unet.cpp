@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <stdexcept>
 
 #include "check.hpp"
@@ -460,6 +461,8 @@ void UNet::pack_all(void* stream) {
   const int T = c.time_dim();
   res_.clear();
   t2d_.clear();
+  res_names_.clear();
+  t2d_names_.clear();
   kv_total_ = 0;
   tproj_total_ = 0;
   cursor_ = 0;
@@ -474,11 +477,15 @@ void UNet::pack_all(void* stream) {
   ae2b_ = copy_of("add_embedding.linear_2.bias", {T}, stream);
 
   auto R = [&](const std::string& p, int Ci, int Co) {
+    res_names_.push_back(p);
     res_.push_back(pack_resnet(p, Ci, Co, stream));
     res_.back().tproj_off = tproj_total_;
     tproj_total_ += Co;
   };
-  auto A = [&](const std::string& p, int C, int depth) { t2d_.push_back(pack_t2d(p, C, depth, stream)); };
+  auto A = [&](const std::string& p, int C, int depth) {
+    t2d_names_.push_back(p);
+    t2d_.push_back(pack_t2d(p, C, depth, stream));
+  };
 
   R("down_blocks.0.resnets.0.", c.C0, c.C0);
   R("down_blocks.0.resnets.1.", c.C0, c.C0);
@@ -718,10 +725,101 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
   }
 }
 
+void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int HW,
+                  const CrossKV& kv, int kv_off, int kv_stride, int ctx_len, void* stream) {
+  const int M = B * HW;
+  const int heads = C / 64;
+  const float scale = 1.0f / std::sqrt(64.0f);
+  void* n = ts.n;
+  void* qkv = ts.qkv;
+  void* vt = ts.vt;
+  const int vt_ld = ts.vt_ld;
+  void* o = ts.o;
+  void* f = ts.f;
+  // self-attention
+  LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
+  // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
+  LAUNCH(kLinear, 2.0 * M * 3 * C * C, 0.0,
+         dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, vt_ld, M,
+                            3 * C, C, stream));
+  {
+    dlm_attention_vt_args a{};
+    const char* base = static_cast<const char*>(qkv);
+    a.q = base;
+    a.k = base + (size_t)C * kH;
+    a.vt = vt;
+    a.q_sb = a.k_sb = (long long)HW * 2 * C;
+    a.q_ss = a.k_ss = 2 * C;
+    a.q_sh = a.k_sh = 64;
+    a.vt_sb = (long long)C * vt_ld;
+    a.vt_sh = 64LL * vt_ld;
+    a.vt_ld = vt_ld;
+    a.o = o;
+    a.o_sb = (long long)HW * C;
+    a.o_ss = C;
+    a.o_sh = 64;
+    a.B = B;
+    a.H = heads;
+    a.Sq = HW;
+    a.Sk = HW;
+    a.scale = scale;
+    a.k_bytes = ((size_t)M * 2 * C - C) * kH;
+    a.vt_bytes = (size_t)B * C * vt_ld * kH;
+    LAUNCH(kAttention, 4.0 * B * heads * (double)HW * HW * 64, 0.0,
+           dlm_attention_vt_fp16(&a, stream));
+  }
+  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+       dlm_linear_fp16(o, C, k.wo1, C, k.bo1, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
+                           stream));
+  // cross-attention over the context's K / V^T (rows kv_off.. of stride kv_stride)
+  LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln2g, k.ln2b, n, M, C, 1e-5f, stream));
+  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+       dlm_linear_fp16(n, C, k.wq2, C, nullptr, nullptr, 0, qkv, C, M, C, C, 1.0f, 0.0f,
+                           DLM_ACT_NONE, stream));
+  {
+    dlm_attention_vt_args a{};
+    a.q = qkv;
+    a.q_sb = (long long)HW * C;
+    a.q_ss = C;
+    a.q_sh = 64;
+    a.k = static_cast<const char*>(kv.k) + (size_t)kv_off * kH;
+    a.k_sb = (long long)ctx_len * kv_stride;
+    a.k_ss = kv_stride;
+    a.k_sh = 64;
+    a.vt = static_cast<const char*>(kv.vt) + (size_t)kv_off * kv.ld * kH;
+    a.vt_sb = (long long)kv_stride * kv.ld;
+    a.vt_sh = 64LL * kv.ld;
+    a.vt_ld = kv.ld;
+    a.o = o;
+    a.o_sb = (long long)HW * C;
+    a.o_ss = C;
+    a.o_sh = 64;
+    a.B = B;
+    a.H = heads;
+    a.Sq = HW;
+    a.Sk = ctx_len;
+    a.scale = scale;
+    a.k_bytes = ((size_t)B * ctx_len * kv_stride - kv_off) * kH;
+    a.vt_bytes = ((size_t)B * kv_stride - kv_off) * kv.ld * kH;
+    LAUNCH(kAttention, 4.0 * B * heads * (double)HW * ctx_len * 64, 0.0,
+           dlm_attention_vt_fp16(&a, stream));
+  }
+  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+       dlm_linear_fp16(o, C, k.wo2, C, k.bo2, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
+                           stream));
+  // GEGLU feed-forward
+  LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln3g, k.ln3b, n, M, C, 1e-5f, stream));
+  LAUNCH(kLinear, 2.0 * M * 8 * C * C, 0.0,
+       dlm_linear_fp16(n, C, k.wff1, C, k.bff1, nullptr, 0, f, 4 * C, M, 8 * C, C, 1.0f,
+                           0.0f, DLM_ACT_GEGLU, stream));
+  LAUNCH(kLinear, 2.0 * M * 4 * C * C, 0.0,
+       dlm_linear_fp16(f, 4 * C, k.wff2, 4 * C, k.bff2, h, C, h, C, M, C, 4 * C, 1.0f, 1.0f,
+                           DLM_ACT_NONE, stream));
+}
+
 void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream) {
   const int C = t.C;
   const int M = B * HW;
-  const int heads = C / 64;
   DeviceArenaScope sc(DeviceArenaId::UNet);
   void* g = sc.alloc<uint16_t>((size_t)M * C);
   void* h = sc.alloc<uint16_t>((size_t)M * C);
@@ -733,98 +831,84 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
   void* vt = sc.alloc<uint16_t>((size_t)B * C * vt_ld);
   void* o = sc.alloc<uint16_t>((size_t)M * C);
   void* f = sc.alloc<uint16_t>((size_t)M * 4 * C);
-  const float scale = 1.0f / std::sqrt(64.0f);
 
   gn(x, C, nullptr, 0, t.ng, t.nb, g, B, HW, 1e-6f, false, stream);
   LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
          dlm_linear_fp16(g, C, t.pin_w, C, t.pin_b, nullptr, 0, h, C, M, C, C, 1.0f, 0.0f,
                            DLM_ACT_NONE, stream));
-  for (const Block& k : t.blocks) {
-    // self-attention
-    LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
-    // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
-    LAUNCH(kLinear, 2.0 * M * 3 * C * C, 0.0,
-           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, vt_ld, M,
-                              3 * C, C, stream));
-    {
-      dlm_attention_vt_args a{};
-      const char* base = static_cast<const char*>(qkv);
-      a.q = base;
-      a.k = base + (size_t)C * kH;
-      a.vt = vt;
-      a.q_sb = a.k_sb = (long long)HW * 2 * C;
-      a.q_ss = a.k_ss = 2 * C;
-      a.q_sh = a.k_sh = 64;
-      a.vt_sb = (long long)C * vt_ld;
-      a.vt_sh = 64LL * vt_ld;
-      a.vt_ld = vt_ld;
-      a.o = o;
-      a.o_sb = (long long)HW * C;
-      a.o_ss = C;
-      a.o_sh = 64;
-      a.B = B;
-      a.H = heads;
-      a.Sq = HW;
-      a.Sk = HW;
-      a.scale = scale;
-      a.k_bytes = ((size_t)M * 2 * C - C) * kH;
-      a.vt_bytes = (size_t)B * C * vt_ld * kH;
-      LAUNCH(kAttention, 4.0 * B * heads * (double)HW * HW * 64, 0.0,
-             dlm_attention_vt_fp16(&a, stream));
-    }
-    LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
-         dlm_linear_fp16(o, C, k.wo1, C, k.bo1, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
-                             stream));
-    // cross-attention (K/V precomputed for all blocks)
-    LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln2g, k.ln2b, n, M, C, 1e-5f, stream));
-    LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
-         dlm_linear_fp16(n, C, k.wq2, C, nullptr, nullptr, 0, qkv, C, M, C, C, 1.0f, 0.0f,
-                             DLM_ACT_NONE, stream));
-    {
-      const int kv_half = kv_total_ / 2;
-      dlm_attention_vt_args a{};
-      a.q = qkv;
-      a.q_sb = (long long)HW * C;
-      a.q_ss = C;
-      a.q_sh = 64;
-      a.k = static_cast<const char*>(kv.k) + (size_t)k.kv_off * kH;
-      a.k_sb = (long long)ctx_len * kv_half;
-      a.k_ss = kv_half;
-      a.k_sh = 64;
-      a.vt = static_cast<const char*>(kv.vt) + (size_t)k.kv_off * kv.ld * kH;
-      a.vt_sb = (long long)kv_half * kv.ld;
-      a.vt_sh = 64LL * kv.ld;
-      a.vt_ld = kv.ld;
-      a.o = o;
-      a.o_sb = (long long)HW * C;
-      a.o_ss = C;
-      a.o_sh = 64;
-      a.B = B;
-      a.H = heads;
-      a.Sq = HW;
-      a.Sk = ctx_len;
-      a.scale = scale;
-      a.k_bytes = ((size_t)B * ctx_len * kv_half - k.kv_off) * kH;
-      a.vt_bytes = ((size_t)B * kv_half - k.kv_off) * kv.ld * kH;
-      LAUNCH(kAttention, 4.0 * B * heads * (double)HW * ctx_len * 64, 0.0,
-             dlm_attention_vt_fp16(&a, stream));
-    }
-    LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
-         dlm_linear_fp16(o, C, k.wo2, C, k.bo2, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
-                             stream));
-    // GEGLU feed-forward
-    LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln3g, k.ln3b, n, M, C, 1e-5f, stream));
-    LAUNCH(kLinear, 2.0 * M * 8 * C * C, 0.0,
-         dlm_linear_fp16(n, C, k.wff1, C, k.bff1, nullptr, 0, f, 4 * C, M, 8 * C, C, 1.0f,
-                             0.0f, DLM_ACT_GEGLU, stream));
-    LAUNCH(kLinear, 2.0 * M * 4 * C * C, 0.0,
-         dlm_linear_fp16(f, 4 * C, k.wff2, 4 * C, k.bff2, h, C, h, C, M, C, 4 * C, 1.0f, 1.0f,
-                             DLM_ACT_NONE, stream));
-  }
+  const TScratch ts{n, qkv, vt, vt_ld, o, f};
+  for (const Block& k : t.blocks) tblock(k, C, h, ts, B, HW, kv, k.kv_off, kv_total_ / 2, ctx_len, stream);
   // proj_out + residual (the block input), written back in place
   LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
          dlm_linear_fp16(h, C, t.pout_w, C, t.pout_b, x, C, x, C, M, C, C, 1.0f, 1.0f,
                            DLM_ACT_NONE, stream));
+}
+
+static std::string with_dot(const std::string& p) {
+  return (!p.empty() && p.back() == '.') ? p : p + ".";
+}
+
+void UNet::run_resnet(const std::string& prefix, const void* xa, int Ca, const void* xb, int Cb,
+                      void* out, int B, int H, int W, const void* temb, void* stream) {
+  if (!packed_) throw std::runtime_error("UNet::run_resnet: prepare() has not run");
+  if (!xa || !out || !temb || (Cb > 0 && !xb)) throw std::invalid_argument("UNet::run_resnet: NULL input");
+  if (B <= 0 || H <= 0 || W <= 0) throw std::invalid_argument("UNet::run_resnet: bad shape");
+  const std::string p = with_dot(prefix);
+  size_t i = 0;
+  while (i < res_names_.size() && res_names_[i] != p) ++i;
+  if (i == res_names_.size()) throw std::out_of_range("UNet::run_resnet: no resnet '" + prefix + "'");
+  const Resnet& r = res_[i];
+  if (Ca + Cb != r.Ci) throw std::invalid_argument("UNet::run_resnet: input channels != block input");
+  const int T = cfg_.time_dim();
+  DeviceArenaScope persist(DeviceArenaId::UNetPersist);
+  // this block's time_emb_proj(silu(temb)), laid out as the forward's tproj
+  // rows would be (row stride tproj_total_, the block's columns at tproj_off)
+  void* tproj = persist.alloc<uint16_t>((size_t)B * tproj_total_);
+  const char* w = static_cast<const char*>(tproj_w_) + (size_t)r.tproj_off * T * kH;
+  const char* b = static_cast<const char*>(tproj_b_) + (size_t)r.tproj_off * kH;
+  DLM_CALL(dlm_linear_small_fp16(temb, T, w, b, static_cast<char*>(tproj) + (size_t)r.tproj_off * kH,
+                                 tproj_total_, B, r.Co, T, 1, DLM_ACT_NONE, 0, stream));
+  resnet(r, xa, Ca, xb, Cb, out, B, H, W, tproj, stream);
+}
+
+void UNet::run_transformer_block(const std::string& prefix, void* x, int B, int HW, const void* ehs,
+                                 int ctx_len, void* stream) {
+  if (!packed_) throw std::runtime_error("UNet::run_transformer_block: prepare() has not run");
+  if (!x || !ehs) throw std::invalid_argument("UNet::run_transformer_block: NULL input");
+  if (B <= 0 || HW <= 0 || ctx_len <= 0) throw std::invalid_argument("UNet::run_transformer_block: bad shape");
+  const std::string p = with_dot(prefix);
+  const std::string tag = "transformer_blocks.";
+  const size_t at = p.rfind(tag);
+  if (at == std::string::npos) throw std::out_of_range("UNet::run_transformer_block: not a block prefix");
+  const std::string owner = p.substr(0, at);
+  const int l = std::atoi(p.c_str() + at + tag.size());
+  size_t ti = 0;
+  while (ti < t2d_names_.size() && t2d_names_[ti] != owner) ++ti;
+  if (ti == t2d_names_.size() || l < 0 || l >= (int)t2d_[ti].blocks.size())
+    throw std::out_of_range("UNet::run_transformer_block: no block '" + prefix + "'");
+  const T2D& t = t2d_[ti];
+  const Block& k = t.blocks[l];
+  const int C = t.C, M = B * HW, cross = cfg_.cross_dim;
+  const int kv_half = kv_total_ / 2;
+  DeviceArenaScope sc(DeviceArenaId::UNet);
+  // this block's context K [B*ctx, C] and V^T [B, C, ctx_pad] from its rows
+  // of the concatenated projection weight
+  const int ctx_pad = (ctx_len + 7) & ~7;
+  CrossKV kv{sc.alloc<uint16_t>((size_t)B * ctx_len * C), sc.alloc<uint16_t>((size_t)B * C * ctx_pad),
+             ctx_pad};
+  const char* kw = static_cast<const char*>(kv_w_) + (size_t)k.kv_off * cross * kH;
+  const char* vw = static_cast<const char*>(kv_w_) + (size_t)(kv_half + k.kv_off) * cross * kH;
+  LAUNCH(kLinear, 2.0 * B * ctx_len * C * cross, 0.0,
+         dlm_linear_fp16(ehs, cross, kw, cross, nullptr, nullptr, 0, kv.k, C, B * ctx_len, C, cross,
+                         1.0f, 0.0f, DLM_ACT_NONE, stream));
+  LAUNCH(kLinear, 2.0 * B * ctx_len * C * cross, 0.0,
+         dlm_linear_vt_fp16(ehs, cross, vw, cross, nullptr, kv.vt, 0, kv.vt, 0, ctx_len, ctx_pad,
+                            B * ctx_len, C, cross, stream));
+  const int vt_ld = (HW + 7) & ~7;
+  const TScratch ts{sc.alloc<uint16_t>((size_t)M * C), sc.alloc<uint16_t>((size_t)M * 2 * C),
+                    sc.alloc<uint16_t>((size_t)B * C * vt_ld), vt_ld,
+                    sc.alloc<uint16_t>((size_t)M * C), sc.alloc<uint16_t>((size_t)M * 4 * C)};
+  tblock(k, C, x, ts, B, HW, kv, 0, C, ctx_len, stream);
 }
 
 void UNet::forward(int B, int H, int W, const void* latent, const float* d_timesteps,

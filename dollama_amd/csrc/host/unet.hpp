@@ -93,6 +93,20 @@ class UNet {
   // bytes must equal 2 * its element count.  Synchronises the stream.
   void read_weight(const std::string& key, void* host, size_t bytes, void* stream) const;
 
+  // One block of the prepared model on its own (block-level tests and
+  // timing; the forward does not use these):
+  //   run_resnet: prefix "down_blocks.1.resnets.0" style; x = concat(xa[:, :Ca],
+  //   xb[:, :Cb]) channels-last [B, H, W, Ca + Cb]; temb [B, time_dim] fp16 as
+  //   the time MLP outputs it (SiLU and this block's time_emb_proj applied
+  //   here); out [B, H, W, Co].
+  //   run_transformer_block: prefix "...attentions.a.transformer_blocks.l";
+  //   x [B * HW, C] updated in place; ehs [B, ctx_len, cross_dim] (the block's
+  //   cross-attention K / V projections are computed here).
+  void run_resnet(const std::string& prefix, const void* xa, int Ca, const void* xb, int Cb,
+                  void* out, int B, int H, int W, const void* temb, void* stream);
+  void run_transformer_block(const std::string& prefix, void* x, int B, int HW, const void* ehs,
+                             int ctx_len, void* stream);
+
   void set_stage_hook(UnetStageHook hook, void* user) {
     hook_ = hook;
     hook_user_ = user;
@@ -196,6 +210,16 @@ class UNet {
     int ld;
   };
   void t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream);
+  // one BasicTransformerBlock over the residual stream h [B*HW, C]; this
+  // block's context K rows start at row kv_off of kv.k (row stride kv_stride)
+  // and its V^T rows at row kv_off of kv.vt (kv_stride rows per sample)
+  struct TScratch {
+    void *n, *qkv, *vt;
+    int vt_ld;
+    void *o, *f;
+  };
+  void tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int HW, const CrossKV& kv,
+              int kv_off, int kv_stride, int ctx_len, void* stream);
   void gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, const void* b, void* out,
           int B, int HW, float eps, bool silu, void* stream);
   void conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, void* out, int Co, int B,
@@ -216,6 +240,7 @@ class UNet {
   int tproj_total_ = 0, kv_total_ = 0;
   std::vector<Resnet> res_;  // in forward order
   std::vector<T2D> t2d_;     // in forward order
+  std::vector<std::string> res_names_, t2d_names_;  // their weight-name prefixes
   UnetStageHook hook_ = nullptr;
   void* hook_user_ = nullptr;
 

@@ -75,6 +75,8 @@ HOST_SIGNATURES = {
     "dlm_f32_to_f16": (I, [P, P, c_size_t]),
     "dlm_arena_stats": (I, [I, POINTER(c_uint64)]),
     "dlm_arena_fill": (I, [I, I]),
+    "dlm_unet_run_resnet": (I, [P, ctypes.c_char_p, P, I, P, I, P, I, I, I, P, P]),
+    "dlm_unet_run_transformer_block": (I, [P, ctypes.c_char_p, P, I, I, P, I, P]),
     "dlm_arena_release": (I, [I]),
     "dlm_arena_reserve": (I, [I, c_size_t]),
 }
@@ -249,6 +251,47 @@ class UNet:
               c_void_p(timesteps.data_ptr()), c_void_p(ehs.data_ptr()), L, c_void_p(text.data_ptr()),
               c_void_p(time_ids.data_ptr()), ids_stride, c_void_p(out.data_ptr()), _stream())
         return out
+
+    def run_resnet(self, prefix: str, x: torch.Tensor, temb: torch.Tensor,
+                   x_b: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+        """One ResnetBlock2D of the prepared model: x [B,H,W,Ca] (+ x_b [B,H,W,Cb]
+        concatenated) channels-last fp16, temb [B, time_dim] fp16 (the time MLP
+        output, before SiLU) -> [B,H,W,Co]."""
+        B, H, W, Ca = x.shape
+        Cb = 0 if x_b is None else x_b.shape[3]
+        T = 4 * self.cfg.C0
+        ts = [(x, (B, H, W, Ca)), (temb, (B, T))] + ([] if x_b is None else [(x_b, (B, H, W, Cb))])
+        for t, shp in ts:
+            if not t.is_cuda or t.dtype != torch.float16 or not t.is_contiguous() or tuple(t.shape) != shp:
+                raise ValueError(f"expected a contiguous fp16 GPU tensor of shape {shp}")
+        co = self._resnet_out_channels(prefix)
+        if out is None:
+            out = torch.empty(B, H, W, co, dtype=torch.float16, device=x.device)
+        if not out.is_contiguous() or tuple(out.shape) != (B, H, W, co):
+            raise ValueError("bad out tensor")
+        _call("dlm_unet_run_resnet", self._h, prefix.encode(), c_void_p(x.data_ptr()), Ca,
+              c_void_p(0 if x_b is None else x_b.data_ptr()), Cb, c_void_p(out.data_ptr()), B, H, W,
+              c_void_p(temb.data_ptr()), _stream())
+        return out
+
+    def _resnet_out_channels(self, prefix: str) -> int:
+        p = prefix.rstrip(".") + ".conv1.weight"
+        shape = dict(weight_specs(self.cfg)).get(p)
+        if shape is None:
+            raise KeyError(f"no resnet '{prefix}'")
+        return shape[0]
+
+    def run_transformer_block(self, prefix: str, x: torch.Tensor, ehs: torch.Tensor) -> torch.Tensor:
+        """One BasicTransformerBlock of the prepared model on x [B, S, C] fp16
+        (updated in place and returned); ehs [B, L, cross_dim] fp16."""
+        B, S, C = x.shape
+        L = ehs.shape[1]
+        for t, shp in ((x, (B, S, C)), (ehs, (B, L, self.cfg.cross_dim))):
+            if not t.is_cuda or t.dtype != torch.float16 or not t.is_contiguous() or tuple(t.shape) != shp:
+                raise ValueError(f"expected a contiguous fp16 GPU tensor of shape {shp}")
+        _call("dlm_unet_run_transformer_block", self._h, prefix.encode(), c_void_p(x.data_ptr()), B, S,
+              c_void_p(ehs.data_ptr()), L, _stream())
+        return x
 
     def apply_lora(self, key: str, A: torch.Tensor, B: torch.Tensor, scale: float):
         """W += scale * (B @ A) on the resident weight `key` (diffusers name);

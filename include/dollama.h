@@ -64,6 +64,24 @@ int dlm_unet_forward(void* handle, int B, int H, int W, const void* latent,
                      const float* timesteps, const void* ehs, int ctx_len, const void* text,
                      const void* time_ids, int ids_bstride, void* out, void* stream);
 
+/* One block of the prepared model on its own, for block-level tests and
+ * timing (the reference's resnet_block / transformer_block,
+ * src/infer/unet.cu:537-797, are file-local; these run the same code the
+ * forward runs for that block).
+ *   dlm_unet_run_resnet: prefix e.g. "down_blocks.1.resnets.0"; input
+ *   channels-last concat(xa [B,H,W,Ca], xb [B,H,W,Cb]) (xb NULL when Cb = 0);
+ *   temb [B, time_dim] fp16 before the SiLU (the time MLP's output; SiLU and
+ *   the block's time_emb_proj are applied inside); out [B,H,W,Co].
+ *   dlm_unet_run_transformer_block: prefix e.g.
+ *   "down_blocks.1.attentions.0.transformer_blocks.0"; x [B*HW, C] updated in
+ *   place; ehs [B, ctx_len, cross_dim] (the block's cross K / V projections
+ *   run inside).
+ * An unknown prefix is DLM_ERR_NOT_FOUND. */
+int dlm_unet_run_resnet(void* handle, const char* prefix, const void* xa, int Ca, const void* xb,
+                        int Cb, void* out, int B, int H, int W, const void* temb, void* stream);
+int dlm_unet_run_transformer_block(void* handle, const char* prefix, void* x, int B, int HW,
+                                   const void* ehs, int ctx_len, void* stream);
+
 /* Runtime LoRA (reference src/infer/unet.cuh:97-114, unet.cu:373-458):
  * W += scale * (B @ A) on the resident weight named base_key (diffusers
  * name), A device fp16 [rank, in_flat], B device fp16 [out_dim, rank]
