@@ -3,14 +3,23 @@
 B=2, fp16 with fp32 accumulation, random-init weights of the SDXL
 architecture (N(0, 0.02^2)), synthetic inputs, on one MI355X.
 
-Prints one JSON line.  ``value`` is the mean wall time of one full UNet step
-(ms, lower is better) over ``--steps`` timed forwards with all inputs
-resident in HBM.  Extra fields report, from device events around every
-launch of a separately profiled forward, each kernel class's time and
-algorithmic TFLOP/s, the conv+attention fraction of the fp16 MFMA peak, the
-roofline of the dominant kernel class, a 20-step CFG Euler denoise loop
-timed on the device, and the fp32 CPU oracle timed on this host's cores
-over a bounded sample (the mid block), scaled to one step by FLOPs.
+Prints one JSON line.  ``value`` is the mean device time of one full UNet step
+(ms, lower is better) over ``--steps`` timed forwards (HIP-graph replays)
+with all inputs resident in HBM.  Extra fields:
+- per kernel class and per kernel instantiation, time and algorithmic
+  TFLOP/s from device events around every launch of separately profiled
+  forwards (on the stream the kernels run on);
+- ``roofline``: the single kernel instantiation with the most time, its
+  algorithmic FLOPs per launch over its average launch duration against the
+  fp16 MFMA peak, and its HBM bytes per launch from rocprofv3 PMC counters
+  (profiles/hbm_traffic.json);
+- ``configs``: the other benchmark configurations timed on their own (single
+  3x3 conv, three ResnetBlock2D shapes, the two self-attention shapes, one
+  BasicTransformerBlock);
+- a 20-step CFG Euler loop on the device;
+- ``cpu_baseline``: the fp32 CPU oracle running one full step of the same
+  workload (same weights and inputs) on this host, with its noise_pred
+  compared against the GPU's.
 """
 import argparse
 import json
@@ -35,6 +44,7 @@ def parse():
     ap.add_argument("--loop-steps", type=int, default=20, help="Euler loop length (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-runs", type=int, default=3)
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config timings")
     ap.add_argument("--eager", action="store_true",
                     help="time eager forwards only (default: HIP-graph replay, eager timed beside it)")
     ap.add_argument("--workload", choices=("unet", "vae"), default="unet",
@@ -59,63 +69,197 @@ def calibrate_copy():
 
 
 def measured_traffic():
-    """HBM bytes per launch of the dominant kernel class, as measured by
-    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this bench and scaled by the
-    same counters on a plain copy (profiles/hbm_traffic.json)."""
+    """HBM bytes per launch by kernel instantiation, from rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE runs on this bench scaled by the same counters on a
+    plain copy (profiles/hbm_traffic.json)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     if not os.path.exists(path):
         return {}
     with open(path) as f:
-        return json.load(f)
+        return json.load(f).get("kernels", {})
 
 
-def cpu_baseline(seed):
-    """fp32 torch-CPU oracle over the mid block (resnet, Transformer2D depth 10,
-    resnet at 32x32x1280, B=2), scaled to a full step by algorithmic FLOPs."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(w_cpu, inputs, gpu_out):
+    """One full UNet step of the same workload (same weights, same fp16 inputs)
+    through the fp32 torch-CPU oracle on this host's CPU share, after a warm-up
+    forward on a 32x32 latent; the oracle's noise_pred is compared with the
+    GPU's (SSIM of the reference's definition, relative error)."""
     import torch
+    from oracle import metrics
     from oracle import unet_ref as OR
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
-    cfg = OR.SDXL
-    shapes = {k: v for k, v in OR.param_shapes(cfg).items() if k.startswith("mid_block.")}
-    g = torch.Generator().manual_seed(seed)
-    W = {}
-    for k, shp in shapes.items():
-        t = torch.randn(shp, generator=g) * 0.02
-        if "norm" in k.split(".")[-2] and k.endswith(".weight") and len(shp) == 1:
-            t += 1.0
-        W[k] = t
-    B, C, Hh = 2, cfg.C2, 32
-    x = torch.randn(B, C, Hh, Hh, generator=g)
-    ctx = torch.randn(B, 77, cfg.cross_dim, generator=g)
-    temb = torch.randn(B, cfg.T, generator=g)
-    ts = OR.R.silu(temb)
-
-    def run():
-        with torch.no_grad():
-            y = OR.resnet_block(W, "mid_block.resnets.0.", x, ts)
-            y = OR.transformer2d(W, "mid_block.attentions.0.", y, ctx, cfg.depth2)
-            return OR.resnet_block(W, "mid_block.resnets.1.", y, ts)
-
-    run()  # warm
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    sec = sorted(times)[1]
-    from dollama_amd.flops import unet_step_flops, mid_block_flops
-    full = unet_step_flops(B=2, H=128, W=128)["total"]
-    mid = mid_block_flops(B=2)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    lat, ts, ehs, text, ids = inputs
+    OR.unet_forward(w_cpu, OR.SDXL, lat[:, :, :32, :32].contiguous(), ts, ehs, text, ids)
+    t0 = time.perf_counter()
+    ref = OR.unet_forward(w_cpu, OR.SDXL, lat, ts, ehs, text, ids)
+    sec = time.perf_counter() - t0
+    got = gpu_out.float().cpu()
     return {
-        "value": sec * (full / mid) * 1e3,
-        "unit": "ms/step (scaled)",
-        "cores": cores,
+        "value": round(sec * 1e3, 1),
+        "unit": "ms/step",
+        "cores": threads,
         "kind": "port",
-        "sample": f"oracle mid_block (resnet + Transformer2D depth 10 + resnet, B=2, 32x32x1280, "
-                  f"{mid / 1e12:.3f} TFLOP) median of 3 = {sec * 1e3:.0f} ms, scaled by "
-                  f"{full / 1e12:.3f}/{mid / 1e12:.3f} TFLOP",
+        "sample": "one full SDXL UNet step (B=2, latent 128x128, ctx 77x2048) through the fp32 "
+                  "torch-CPU oracle with the GPU run's weights and inputs, after a 32x32 warm-up",
+        "cpu_model": cpu_model(),
+        "host_logical_cpus": os.cpu_count(),
+        "gpu_vs_cpu": {"ssim": round(metrics.ssim_uniform(got, ref), 7),
+                       "rel_err": float(f"{metrics.rel_err(got, ref):.3e}"),
+                       "cosine": round(metrics.cosine(got, ref), 7)},
     }
+
+
+def queue_ahead(seconds=0.01):
+    """Hold the current stream with a spin kernel of about `seconds` so that the
+    work enqueued next runs back to back on the device: event pairs then time
+    the kernels, not the host's launch gaps (the host must finish enqueueing
+    before the spin ends)."""
+    import torch
+    torch.cuda._sleep(int(2.5e9 * seconds))
+
+
+def time_calls(fn, reps=20, warmup=3):
+    """Mean device time (ms) of fn() over reps back-to-back calls between one
+    event pair on the current stream, queued behind a spin kernel."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    queue_ahead(max(0.01, reps * 2e-4))  # 200 us of host time per call at most
+    e0.record(st)
+    for _ in range(reps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def time_graph(fn, reps=20):
+    """Device time (ms) per call of fn() when reps calls are captured into one
+    HIP graph and the graph is replayed between an event pair: back-to-back
+    kernels with the inter-node gap of a graph, as in the graph-replayed step."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def replay_kernel(name, problems, dev, seed):
+    """Average launch duration (us) and FLOPs of one GEMM kernel instantiation
+    over the problems it ran in the step: each problem's launches are captured
+    into a HIP graph and replayed between one event pair (time_graph), and the
+    per-problem times are weighted by the problem's launches per step.  The
+    kernel each launch ran is checked against `name`.  None for convs."""
+    import ctypes
+    import torch
+    from dollama_amd import _lib, ops
+    lib = _lib.hip_lib()
+    lib.dlm_last_kernel.restype = ctypes.c_char_p
+    lib.dlm_last_kernel.argtypes = [ctypes.c_int]
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * std).half()
+
+    tot_us = tot_flop = 0.0
+    tot_n = 0
+    for (M, N, K, flags), cnt in problems.items():
+        if flags & 256:
+            return None
+        act, res = (flags >> 4) & 15, flags & 1
+        ncols = N // 2 if act == ops.ACT_GEGLU else N
+        x, w, b = rn(M, K), rn(N, K, std=0.02), rn(N, std=0.01)
+        r = rn(M, ncols) if res else None
+        y = torch.empty(M, ncols, dtype=torch.float16, device=dev)
+        fn = lambda: ops.linear(x, w, bias=b, residual=r, act=act, out=y)
+        fn()
+        ran = lib.dlm_last_kernel(1).decode()
+        if ran != name:
+            raise RuntimeError(f"replay of {M}x{N}x{K} ran {ran}, not {name}")
+        ms = time_graph(fn, reps=max(20, cnt))
+        tot_us += ms * 1e3 * cnt
+        tot_flop += 2.0 * M * N * K * cnt
+        tot_n += cnt
+    return tot_us / tot_n, tot_flop / tot_n
+
+
+def config_timings(net, U, dev, seed):
+    """The benchmark's other configurations, each timed on its own."""
+    import torch
+    from dollama_amd import ops
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * std).half()
+
+    def entry(ms, flop):
+        return {"ms": round(ms, 4), "tflop": round(flop / 1e12, 4),
+                "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                "frac_mfma": round(flop / (ms * 1e-3) / MFMA_FP16_PEAK, 4)}
+
+    out = {}
+    # 1: conv 3x3 320->320 @128x128, N=1, bias + SiLU epilogue
+    x = rn(1, 128, 128, 320)
+    wp = ops.pack_conv_weight(rn(320, 320, 3, 3, std=0.02))
+    b = rn(320, std=0.01)
+    y = torch.empty(1, 128, 128, 320, dtype=torch.float16, device=dev)
+    ms = time_calls(lambda: ops.conv2d_nhwc(x, wp, KH=3, KW=3, bias=b, act=ops.ACT_SILU, out=y))
+    out["conv3x3_320_128px_n1_bias_silu"] = entry(ms, 2.0 * 16384 * 320 * 2880)
+    # 2: ResnetBlock2D at B=2 (FLOPs of the convs, as the configuration counts them)
+    temb = rn(2, 1280)
+    for name, prefix, ci, co, hw in (("resnet_640ch_64px", "down_blocks.1.resnets.1.", 640, 640, 64),
+                                     ("resnet_1280ch_32px", "mid_block.resnets.0.", 1280, 1280, 32),
+                                     ("resnet_320to640_64px_1x1skip", "down_blocks.1.resnets.0.", 320, 640, 64)):
+        xr = rn(2, hw, hw, ci)
+        yr = torch.empty(2, hw, hw, co, dtype=torch.float16, device=dev)
+        ms = time_calls(lambda: net.run_resnet(prefix, xr, temb, out=yr))
+        flop = 2.0 * 2 * hw * hw * co * (9 * ci + 9 * co + (ci if ci != co else 0))
+        out[name] = entry(ms, flop)
+    # 3: flash self-attention, fp16 with fp32 softmax (V^T form of the UNet)
+    for name, B, H, S in (("attention_b2_h10_s4096", 2, 10, 4096), ("attention_b2_h20_s1024", 2, 20, 1024)):
+        C = H * 64
+        qk = rn(B, S, 2 * C)
+        vt = rn(B, H, 64, S)
+        o = torch.empty(B, S, C, dtype=torch.float16, device=dev)
+        ms = time_calls(lambda: ops.attention_vt(qk, qk[:, :, C:], vt, o, B=B, H=H, Sq=S, Sk=S,
+                                                 q_strides=(S * 2 * C, 2 * C, 64), k_strides=(S * 2 * C, 2 * C, 64),
+                                                 vt_strides=(H * 64 * S, 64 * S), vt_ld=S,
+                                                 o_strides=(S * C, C, 64), scale=0.125))
+        out[name] = entry(ms, 4.0 * B * H * S * S * 64)
+    # 4: BasicTransformerBlock on 2x4096x640, context 2x77x2048 (incl. its K/V projections)
+    xt = rn(2, 4096, 640)  # the block updates it in place on every call
+    ctx = rn(2, 77, 2048)
+    ms = time_calls(lambda: net.run_transformer_block("down_blocks.1.attentions.0.transformer_blocks.0.", xt, ctx))
+    M, C = 8192, 640
+    flop = 2.0 * M * C * C * 18 + 2 * 2.0 * 154 * 2048 * C + 4.0 * 2 * 10 * 4096 * 4096 * 64 + 4.0 * 2 * 10 * 4096 * 77 * 64
+    out["basic_transformer_block_2x4096x640"] = entry(ms, flop)
+    return out
 
 
 def main():
@@ -143,6 +287,8 @@ def main():
     weights = U.random_weights(cfg, args.seed, device=dev)
     net.set_weights(weights)
     net.prepare()
+    # the CPU leg runs the same model: an fp32 host copy of the fp16 weights
+    w_cpu = None if args.no_cpu_baseline else {k: v.float().cpu() for k, v in weights.items()}
     del weights
     torch.cuda.empty_cache()
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
@@ -184,13 +330,21 @@ def main():
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite noise_pred")
 
-    # per-class kernel time from device events around every launch
+    # per-class and per-kernel time from device events around every launch
     net.set_profiling(True)
-    reports = []
+    reports, kreports = [], []
     for _ in range(max(1, args.profile_runs)):
+        queue_ahead(0.03)
         net.forward(latent, ts, ehs, text, ids, out=out)
         reports.append(net.profile_report())
+        kreports.append(net.profile_kernels())
     net.set_profiling(False)
+    kernels = {}
+    for name, k0 in kreports[-1].items():
+        ms_k = sorted(r[name]["ms"] for r in kreports)[len(kreports) // 2]
+        kernels[name] = {"class": k0["class"], "launches": k0["launches"], "ms": round(ms_k, 4),
+                         "flops": k0["flops"], "bytes": k0["bytes"],
+                         "tflops": round(k0["flops"] / (ms_k * 1e-3) / 1e12, 1) if k0["flops"] and ms_k else None}
     classes = {}
     for c in U.UNet.KERNEL_CLASSES:
         ms_c = sorted(r[c]["ms"] for r in reports)[len(reports) // 2]
@@ -202,11 +356,24 @@ def main():
     conv_attn_flops = fl["conv"] + fl["attention"]
     conv_attn_ms = classes["conv"]["ms"] + classes["attention"]["ms"]
     kernel_ms = sum(v["ms"] for v in classes.values())
-    dom = max(("conv", "linear", "attention"), key=lambda c: classes[c]["ms"])
-    dom_flops = reports[-1][dom]["flops"]
-    dom_ms = classes[dom]["ms"]
-    dom_launches = classes[dom]["launches"]
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    # the dominant kernel: the one instantiation with the most time among the
+    # MFMA-bound classes
+    dom = max((n for n, k in kernels.items() if k["class"] in ("conv", "linear", "attention")),
+              key=lambda n: kernels[n]["ms"])
+    dk = kernels[dom]
+    bracketed_us = dk["ms"] / dk["launches"] * 1e3
+    # its average launch duration: the step's problems of this kernel replayed
+    # back to back (per-launch event pairs inside the forward add ~3 us each)
+    rp = replay_kernel(dom, kreports[-1][dom]["problems"], dev, args.seed + 3)
+    if rp is not None:
+        dom_avg_us, dom_flop = rp
+        dom_timing = ("the step's launches of this kernel (its GEMM problems, weighted by launches per "
+                      "step) captured into a HIP graph and replayed between device events")
+    else:
+        dom_avg_us, dom_flop = bracketed_us, dk["flops"] / dk["launches"]
+        dom_timing = "device events around each launch of the profiled forwards"
+    achieved = dom_flop / (dom_avg_us * 1e-6) / 1e12
+    traffic = measured_traffic().get(dom, {})
 
     # 20-step CFG Euler denoise loop on the device
     loop = None
@@ -225,7 +392,13 @@ def main():
                 "finite": bool(torch.isfinite(lt).all()), "graphs": not args.eager}
         net.set_graphs(False)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.seed)
+    configs = None if args.no_configs else config_timings(net, U, dev, args.seed + 2)
+
+    cpu = None
+    if w_cpu is not None:
+        inputs = (latent.float().cpu(), ts.cpu(), ehs.float().cpu(), text.float().cpu(), ids.float().cpu())
+        cpu = cpu_baseline(w_cpu, inputs, eager_out)
+        del w_cpu
 
     line = {
         "metric": "SDXL UNet step ms @1024^2 CFG B=2; conv/attn TFLOPS & % fp16 MFMA peak",
@@ -256,18 +429,23 @@ def main():
         "classes": classes,
         "roofline": {
             "bound": "mfma",
-            "kernel": {"conv": "dma_gemm_kernel<ConvDesc> (implicit-GEMM conv, LDS-DMA)",
-                       "linear": "dma_gemm_kernel<RowDesc> (linears, LDS-DMA)",
-                       "attention": "flash_vt_pipe_kernel (self and cross attention)"}[dom],
+            "kernel": dom,
+            "class": dk["class"],
             "achieved": round(achieved, 1),
             "peak": MFMA_FP16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(achieved * 1e12 / MFMA_FP16_PEAK, 4),
-            "traffic": measured_traffic().get(dom, {}).get("hbm_bytes_per_launch"),
-            "launches_per_step": dom_launches,
-            "avg_launch_us": round(dom_ms / max(1, dom_launches) * 1e3, 2),
-            "flop_per_step": dom_flops,
+            "traffic": traffic.get("hbm_bytes_per_launch"),
+            "algorithmic_bytes_per_launch": round(dk["bytes"] / dk["launches"]),
+            "launches_per_step": dk["launches"],
+            "avg_launch_us": round(dom_avg_us, 2),
+            "flop_per_launch": dom_flop,
+            "timing": dom_timing,
+            "in_step_bracketed_avg_launch_us": round(bracketed_us, 2),
         },
+        "kernels": {n: {kk: v for kk, v in k.items() if kk not in ("bytes", "problems")}
+                    for n, k in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])[:12]},
+        "configs": configs,
         "euler_loop": loop,
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),

@@ -521,10 +521,10 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   p.B = a->B;
   if (a->Sk > 2 * FA_TK && (long long)((a->Sq + 127) / 128) * a->H * a->B < 512) {
     p.nqb = (a->Sq + 63) / 64;
-    hipLaunchKernelGGL(flash_vt_pipe_kernel<2>, dim3(p.nqb * p.H * p.B), dim3(128), 0, s, p);
+    DLM_LAUNCH("flash_vt_pipe_kernel<2>", flash_vt_pipe_kernel<2>, dim3(p.nqb * p.H * p.B), dim3(128), 0, s, p);
   } else {
     p.nqb = (a->Sq + 127) / 128;
-    hipLaunchKernelGGL(flash_vt_pipe_kernel<4>, dim3(p.nqb * p.H * p.B), dim3(256), 0, s, p);
+    DLM_LAUNCH("flash_vt_pipe_kernel<4>", flash_vt_pipe_kernel<4>, dim3(p.nqb * p.H * p.B), dim3(256), 0, s, p);
   }
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -544,7 +544,7 @@ int attention_strided(const dlm_attention_args* a, hipStream_t s) {
   p.Sk = a->Sk;
   p.scale_log2 = a->scale * 1.4426950408889634f;
   const dim3 grid((a->Sq + AQ_BLOCK - 1) / AQ_BLOCK, a->H, a->B);
-  hipLaunchKernelGGL(flash_attn_d64_kernel, grid, dim3(256), 0, s, p);
+  DLM_LAUNCH("flash_attn_d64_kernel", flash_attn_d64_kernel, grid, dim3(256), 0, s, p);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -658,11 +658,11 @@ softmax_rows_kernel(const float* __restrict__ S, long long lds, f16* __restrict_
 int softmax_rows(const float* S, long long lds, f16* P, long long ldp, int rows, int cols, int colw,
                  hipStream_t s) {
   if (colw <= 256 * 4 * 4)
-    hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
+    DLM_LAUNCH("softmax_rows_kernel<4>", softmax_rows_kernel<4>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
   else if (colw <= 256 * 4 * 16)
-    hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
+    DLM_LAUNCH("softmax_rows_kernel<16>", softmax_rows_kernel<16>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
   else
-    hipLaunchKernelGGL(softmax_rows_kernel<0>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
+    DLM_LAUNCH("softmax_rows_kernel<0>", softmax_rows_kernel<0>, dim3(rows), dim3(256), 0, s, S, lds, P, ldp, cols, colw);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -714,7 +714,7 @@ __global__ void vt_pad_kernel(const f16* __restrict__ v, f16* __restrict__ out, 
 
 static int vt_pad(const f16* v, f16* out, long long BH, int Sk, int Dh, int ld, hipStream_t s) {
   const dim3 grid((ld + 31) / 32, (Dh + 31) / 32, (unsigned)BH);
-  hipLaunchKernelGGL(vt_pad_kernel, grid, dim3(32, 8), 0, s, v, out, Sk, Dh, ld);
+  DLM_LAUNCH("vt_pad_kernel", vt_pad_kernel, grid, dim3(32, 8), 0, s, v, out, Sk, Dh, ld);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -722,7 +722,7 @@ static int vt_pad(const f16* v, f16* out, long long BH, int Sk, int Dh, int ld, 
 static int pad_rows(const f16* in, f16* out, long long rows, int cols, int ld, hipStream_t s) {
   const long long total = rows * ld;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
-  hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, s, in, out, rows, cols, ld);
+  DLM_LAUNCH("pad_rows_kernel", pad_rows_kernel, dim3(blocks), dim3(256), 0, s, in, out, rows, cols, ld);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

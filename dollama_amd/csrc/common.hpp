@@ -97,7 +97,20 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line);
 // frees the old block, so those entry points are not capturable into a graph
 // until their slots have reached size.
 void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status);
+// Name of the kernel an entry point launches last (per thread), for
+// per-kernel timing attribution (dlm_last_kernel).
+void note_kernel(const char* name);
+// GEMM / conv launches also note their problem: rows M, output columns N,
+// reduction length K, flags (bit 0 residual, bits 4.. epilogue activation,
+// bit 8 implicit-GEMM conv).
+void note_dims(int M, int N, int K, int flags);
 }  // namespace dlm
+
+#define DLM_LAUNCH(name, ...)          \
+  do {                                 \
+    ::dlm::note_kernel(name);          \
+    hipLaunchKernelGGL(__VA_ARGS__);   \
+  } while (0)
 
 #define DLM_HIP(expr)                                                          \
   do {                                                                         \

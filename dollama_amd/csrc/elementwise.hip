@@ -244,7 +244,7 @@ extern "C" {
 int dlm_silu_fp16(const void* in, void* out, int n, void* stream) {
   EW_PRE(n);
   DLM_REQUIRE(in && out, "NULL pointer");
-  hipLaunchKernelGGL(silu_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)in, (f16*)out,
+  DLM_LAUNCH("silu_kernel", silu_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)in, (f16*)out,
                      (long long)n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -253,7 +253,7 @@ int dlm_silu_fp16(const void* in, void* out, int n, void* stream) {
 int dlm_gelu_fp16(const void* in, void* out, int n, void* stream) {
   EW_PRE(n);
   DLM_REQUIRE(in && out, "NULL pointer");
-  hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)in, (f16*)out,
+  DLM_LAUNCH("gelu_kernel", gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)in, (f16*)out,
                      (long long)n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -262,7 +262,7 @@ int dlm_gelu_fp16(const void* in, void* out, int n, void* stream) {
 int dlm_add_fp16(const void* a, const void* b, void* out, int n, void* stream) {
   EW_PRE(n);
   DLM_REQUIRE(a && b && out, "NULL pointer");
-  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)a, (const f16*)b,
+  DLM_LAUNCH("add_kernel", add_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)a, (const f16*)b,
                      (f16*)out, (long long)n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -273,7 +273,7 @@ int dlm_upsample_nearest2x_fp16(const void* in, void* out, int N, int C, int H, 
   if (N <= 0 || C <= 0 || H <= 0 || W <= 0) return DLM_OK;
   DLM_REQUIRE(in && out, "NULL pointer");
   const long long n = (long long)N * C * 4 * H * W;
-  hipLaunchKernelGGL(upsample2x_nchw_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("upsample2x_nchw_kernel", upsample2x_nchw_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)in, (f16*)out, H, W, n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -284,7 +284,7 @@ int dlm_bias_add_rowvec_fp16(const void* in, const void* bias, void* out, int to
   if (tokens <= 0 || C <= 0) return DLM_OK;
   DLM_REQUIRE(in && bias && out, "NULL pointer");
   const long long n = (long long)tokens * C;
-  hipLaunchKernelGGL(bias_rowvec_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("bias_rowvec_kernel", bias_rowvec_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)in, (const f16*)bias, (f16*)out, C, n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -293,7 +293,7 @@ int dlm_bias_add_rowvec_fp16(const void* in, const void* bias, void* out, int to
 static int bias_channel(const void* in, const void* bias, const void* tproj, const void* res,
                         void* out, int N, int C, int HW, void* stream) {
   const long long n = (long long)N * C * HW;
-  hipLaunchKernelGGL(bias_channel_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("bias_channel_kernel", bias_channel_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)in, (const f16*)bias, (const f16*)tproj, (const f16*)res,
                      (f16*)out, C, HW, n);
   DLM_LAUNCH_CHECK();
@@ -326,7 +326,7 @@ int dlm_geglu_fp16(const void* in, void* out, int tokens, int d, void* stream) {
   DLM_REQUIRE(in && out, "NULL pointer");
   DLM_REQUIRE(in != out, "geglu cannot run in place");
   const long long n = (long long)tokens * d;
-  hipLaunchKernelGGL(geglu_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("geglu_kernel", geglu_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)in, (f16*)out, d, n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -338,7 +338,7 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
   DLM_REQUIRE(out != nullptr, "NULL pointer");
   DLM_REQUIRE(max_period > 0.0f, "max_period must be positive");
   const int half = dim / 2;
-  hipLaunchKernelGGL(timestep_embedding_kernel, dim3((half + 255) / 256), dim3(256), 0,
+  DLM_LAUNCH("timestep_embedding_kernel", timestep_embedding_kernel, dim3((half + 255) / 256), dim3(256), 0,
                      (hipStream_t)stream, (f16*)out, timestep, dim, logf(max_period));
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -351,7 +351,7 @@ int dlm_sdxl_embed_inputs_fp16(const float* timesteps, const void* text_embeds, 
   DLM_REQUIRE(timesteps && text_embeds && time_ids && t_emb && add_in, "NULL pointer");
   DLM_REQUIRE(ids_bstride >= 0 && text_dim > 0 && id_dim > 0 && t_dim > 0, "bad dims");
   DLM_REQUIRE(t_dim % 2 == 0 && id_dim % 2 == 0, "embedding dims must be even");
-  hipLaunchKernelGGL(sdxl_embed_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, timesteps,
+  DLM_LAUNCH("sdxl_embed_kernel", sdxl_embed_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, timesteps,
                      (const f16*)text_embeds, text_dim, (const f16*)time_ids, ids_bstride, id_dim,
                      (f16*)t_emb, t_dim, (f16*)add_in);
   DLM_LAUNCH_CHECK();
@@ -367,7 +367,7 @@ int dlm_linear_small_fp16(const void* X, int ldx, const void* W, const void* bia
   DLM_REQUIRE(K % 8 == 0 && ldx % 8 == 0 && ldx >= K && ldy >= N, "bad K / strides");
   DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
   DLM_REQUIRE(act == DLM_ACT_NONE || act == DLM_ACT_SILU, "act must be none or silu");
-  hipLaunchKernelGGL(linear_small_kernel, dim3((N + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("linear_small_kernel", linear_small_kernel, dim3((N + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)X, ldx, (const f16*)W, (const f16*)bias, (f16*)Y, ldy, M, N, K,
                      silu_in, act, accumulate);
   DLM_LAUNCH_CHECK();
@@ -378,7 +378,7 @@ int dlm_euler_cfg_step(float* latent, const void* noise, void* model_in, int n, 
                        float sigma, float sigma_next, float in_scale, void* stream) {
   if (n <= 0) return DLM_OK;
   DLM_REQUIRE(latent && noise && model_in, "NULL pointer");
-  hipLaunchKernelGGL(euler_cfg_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("euler_cfg_kernel", euler_cfg_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      latent, (const f16*)noise, (f16*)model_in, n, guidance, sigma_next - sigma,
                      in_scale);
   DLM_LAUNCH_CHECK();
@@ -389,7 +389,7 @@ int dlm_euler_step(float* latent, const void* noise, void* model_in, int n, floa
                    float sigma_next, float in_scale, void* stream) {
   if (n <= 0) return DLM_OK;
   DLM_REQUIRE(latent && noise && model_in, "NULL pointer");
-  hipLaunchKernelGGL(euler_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, latent,
+  DLM_LAUNCH("euler_kernel", euler_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, latent,
                      (const f16*)noise, (f16*)model_in, n, sigma_next - sigma, in_scale);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -399,7 +399,7 @@ int dlm_cast_f32_to_f16(const float* in, void* out, long long n, float scale, vo
   if (n <= 0) return DLM_OK;
   DLM_REQUIRE(in && out, "NULL pointer");
   DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(out), "buffers must be 16-byte aligned");
-  hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(grid_for(std::max(n >> 3, 1LL))), dim3(256), 0,
+  DLM_LAUNCH("cast_f32_f16_kernel", cast_f32_f16_kernel, dim3(grid_for(std::max(n >> 3, 1LL))), dim3(256), 0,
                      (hipStream_t)stream, in, (f16*)out, n, scale);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -408,7 +408,7 @@ int dlm_cast_f32_to_f16(const float* in, void* out, long long n, float scale, vo
 int dlm_scale_fp16(void* x, long long n, float scale, void* stream) {
   if (n <= 0) return DLM_OK;
   DLM_REQUIRE(x, "NULL pointer");
-  hipLaunchKernelGGL(scale_f16_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("scale_f16_kernel", scale_f16_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      (f16*)x, n, scale);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -419,7 +419,7 @@ int dlm_latent_to_vae_fp16(const float* latent, void* out, long long n, float sc
   if (n <= 0) return DLM_OK;
   DLM_REQUIRE(latent && out, "NULL pointer");
   DLM_REQUIRE(scaling_factor != 0.0f, "scaling_factor must be non-zero");
-  hipLaunchKernelGGL(latent_to_vae_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("latent_to_vae_kernel", latent_to_vae_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      latent, (f16*)out, n, scaling_factor);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -429,7 +429,7 @@ int dlm_image_to_rgb8(const void* image, uint8_t* rgb, int N, int H, int W, void
   if (N <= 0 || H <= 0 || W <= 0) return DLM_OK;
   DLM_REQUIRE(image && rgb, "NULL pointer");
   const long long HW = (long long)H * W, n = (long long)N * HW * 3;
-  hipLaunchKernelGGL(image_to_rgb8_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("image_to_rgb8_kernel", image_to_rgb8_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)image, rgb, HW, n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -439,7 +439,7 @@ int dlm_scale_latent_fp16(const float* latent, void* model_in, int n, float scal
                           void* stream) {
   if (n <= 0 || copies <= 0) return DLM_OK;
   DLM_REQUIRE(latent && model_in, "NULL pointer");
-  hipLaunchKernelGGL(scale_latent_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("scale_latent_kernel", scale_latent_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
                      latent, (f16*)model_in, n, scale, copies);
   DLM_LAUNCH_CHECK();
   return DLM_OK;

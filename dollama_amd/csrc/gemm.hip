@@ -1147,6 +1147,25 @@ struct NoSplitScope {
   ~NoSplitScope() { t_no_split = prev; }
 };
 
+// "dma_gemm_kernel<BM, BN, WM, WN, NS, PF, RowDesc|ConvDesc>", as the
+// profiler prints the instantiation
+template <int BM, int BN, int WM, int WN, int NS, bool PF, class Desc>
+static const char* dma_kernel_name() {
+  static const std::string n = "dma_gemm_kernel<" + std::to_string(BM) + ", " + std::to_string(BN) +
+                               ", " + std::to_string(WM) + ", " + std::to_string(WN) + ", " +
+                               std::to_string(NS) + ", " + (PF ? "true" : "false") + ", " +
+                               (std::is_same<Desc, RowDesc>::value ? "RowDesc" : "ConvDesc") + ">";
+  return n.c_str();
+}
+template <int BM, int BN, int WM, int WN, bool DEEP, class Desc>
+static const char* mfma_kernel_name() {
+  static const std::string n = "mfma_gemm_kernel<" + std::to_string(BM) + ", " + std::to_string(BN) +
+                               ", " + std::to_string(WM) + ", " + std::to_string(WN) + ", " +
+                               (DEEP ? "true" : "false") + ", " +
+                               (std::is_same<Desc, RowDesc>::value ? "RowDesc" : "ConvDesc") + ">";
+  return n.c_str();
+}
+
 template <int BM, int BN, int WM, int WN, int NS, bool PF = false, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                       hipStream_t s, int S = 1) {
@@ -1167,6 +1186,8 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   }
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
   const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
+  note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, Desc>());
+  note_dims(M, N, bd.K, (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0));
   hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, Desc>), dim3(grid), dim3(NT), 0, s, ad,
                      bd, ep, tiles_m, tiles_n, sp);
   DLM_LAUNCH_CHECK();
@@ -1179,6 +1200,8 @@ static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  note_kernel(mfma_kernel_name<BM, BN, WM, WN, DEEP, Desc>());
+  note_dims(M, N, bd.K, (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0));
   hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, WM, WN, DEEP, Desc>), dim3(tiles_m * tiles_n),
                      dim3(NT), 0, s, ad, bd, ep, tiles_m, tiles_n);
   DLM_LAUNCH_CHECK();
@@ -1508,7 +1531,7 @@ __global__ void transpose_kernel(const f16* __restrict__ in, f16* __restrict__ o
 
 int nchw_to_nhwc(const void* in, void* out, int N, int C, int HW, int C_pad, hipStream_t s) {
   dim3 grid((HW + 31) / 32, (std::max(C, C_pad) + 31) / 32, N);
-  hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
+  DLM_LAUNCH("nchw_to_nhwc_kernel", nchw_to_nhwc_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
                      HW, C_pad);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -1516,7 +1539,7 @@ int nchw_to_nhwc(const void* in, void* out, int N, int C, int HW, int C_pad, hip
 
 int nhwc_to_nchw(const void* in, void* out, int N, int C, int HW, int C_pad, hipStream_t s) {
   dim3 grid((HW + 31) / 32, (C + 31) / 32, N);
-  hipLaunchKernelGGL(nhwc_to_nchw_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
+  DLM_LAUNCH("nhwc_to_nchw_kernel", nhwc_to_nchw_kernel, grid, dim3(32, 8), 0, s, (const f16*)in, (f16*)out, C,
                      HW, C_pad);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -1526,7 +1549,7 @@ int conv_weight_pack_add(const void* w, void* out, int Cout, int Cin, int KH, in
                          int ld, int col0, hipStream_t s) {
   const long long total = (long long)Cout * KH * KW * Cin;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
-  hipLaunchKernelGGL(conv_weight_pack_add_kernel, dim3(blocks), dim3(256), 0, s, (const f16*)w,
+  DLM_LAUNCH("conv_weight_pack_add_kernel", conv_weight_pack_add_kernel, dim3(blocks), dim3(256), 0, s, (const f16*)w,
                      (f16*)out, Cout, Cin, KH * KW, Cin_pad, ld, col0);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -1536,7 +1559,7 @@ int conv_weight_pack(const void* w, void* out, int Cout, int Cin, int KH, int KW
                      int ld, int col0, hipStream_t s) {
   const long long total = (long long)Cout * KH * KW * Cin_pad;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
-  hipLaunchKernelGGL(conv_weight_pack_kernel, dim3(blocks), dim3(256), 0, s, (const f16*)w,
+  DLM_LAUNCH("conv_weight_pack_kernel", conv_weight_pack_kernel, dim3(blocks), dim3(256), 0, s, (const f16*)w,
                      (f16*)out, Cout, Cin, KH * KW, Cin_pad, ld, col0);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -1705,7 +1728,7 @@ int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, fl
     if (!t) return st;
     DLM_HIP(hipMemsetAsync(t, 0, (size_t)M * Kp * 2, s));
     if (transA) {  // A stored [K, M]
-      hipLaunchKernelGGL(transpose_kernel, dim3((M + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
+      DLM_LAUNCH("transpose_kernel", transpose_kernel, dim3((M + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
                          (const f16*)A, t, K, M, Kp);
       DLM_LAUNCH_CHECK();
     } else {
@@ -1720,7 +1743,7 @@ int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, fl
     if (!t) return st;
     DLM_HIP(hipMemsetAsync(t, 0, (size_t)N * Kp * 2, s));
     if (!transB) {  // B stored [K, N]
-      hipLaunchKernelGGL(transpose_kernel, dim3((N + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
+      DLM_LAUNCH("transpose_kernel", transpose_kernel, dim3((N + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
                          (const f16*)B, t, K, N, Kp);
       DLM_LAUNCH_CHECK();
     } else {
@@ -1739,7 +1762,7 @@ int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias
   if (d <= 0 || K <= 0) return DLM_OK;
   DLM_REQUIRE(w && w_out, "NULL pointer");
   DLM_REQUIRE(d % 4 == 0, "d must be a multiple of 4");
-  hipLaunchKernelGGL(geglu_pack_kernel, dim3(2 * d), dim3(256), 0, (hipStream_t)stream,
+  DLM_LAUNCH("geglu_pack_kernel", geglu_pack_kernel, dim3(2 * d), dim3(256), 0, (hipStream_t)stream,
                      (const f16*)w, (const f16*)bias, (f16*)w_out, (f16*)bias_out, d, K);
   DLM_LAUNCH_CHECK();
   return DLM_OK;

@@ -2,6 +2,8 @@
 // C++ exceptions and turns them into a status plus dlm_last_error() text.
 #include "dollama.h"
 
+#include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -299,6 +301,31 @@ int dlm_unet_profile_report(void* handle, double* out, void* stream) {
       out[4 * c + 1] = r[c].ms;
       out[4 * c + 2] = r[c].flops;
       out[4 * c + 3] = r[c].bytes;
+    }
+  });
+}
+
+int dlm_unet_profile_kernels(void* handle, char* buf, size_t len, size_t* needed, void* stream) {
+  return guarded([&] {
+    if (!handle || !needed) throw std::invalid_argument("NULL argument");
+    std::string text;
+    char line[512];
+    for (const auto& k : static_cast<UNet*>(handle)->profile_kernels(stream)) {
+      std::snprintf(line, sizeof(line), "%s\t%d\t%d\t%.6f\t%.6e\t%.6e\t", k.name.c_str(), k.cls,
+                    k.count, k.ms, k.flops, k.bytes);
+      text += line;
+      for (const auto& d : k.dims) {
+        std::snprintf(line, sizeof(line), "%d,%d,%d,%d:%d;", d.first[0], d.first[1], d.first[2],
+                      d.first[3], d.second);
+        text += line;
+      }
+      text += "\n";
+    }
+    *needed = text.size() + 1;
+    if (buf && len > 0) {
+      const size_t n = std::min(len - 1, text.size());
+      std::memcpy(buf, text.data(), n);
+      buf[n] = 0;
     }
   });
 }

@@ -24,6 +24,12 @@ namespace {
 using Shape = std::vector<int64_t>;
 constexpr size_t kH = 2;  // bytes per fp16
 
+// Algorithmic HBM bytes of one fp16 linear Y[M, Ny] = X[M, K] W[N, K]^T
+// (+ residual [M, Ny]): each operand read once, the output written once.
+double lin_bytes(double M, double N, double K, double Ny, bool residual) {
+  return 2.0 * (M * K + N * K + M * Ny + (residual ? M * Ny : 0.0));
+}
+
 std::string shape_str(const Shape& s) {
   std::string r = "[";
   for (size_t i = 0; i < s.size(); ++i) r += (i ? "," : "") + std::to_string(s[i]);
@@ -258,14 +264,41 @@ void UNet::prof_begin(int cls, double flops, double bytes, void* stream) {
     }
   }
   if (prof_recs_.size() <= prof_next_) prof_recs_.resize(prof_next_ + 1);
-  prof_recs_[prof_next_] = ProfRec{cls, flops, bytes};
+  prof_recs_[prof_next_] = ProfRec{cls, flops, bytes, std::string(), {0, 0, 0, 0}};
+  (void)dlm_last_kernel(1);
   DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2], stream));
 }
 
 void UNet::prof_end(void* stream) {
   if (!prof_on_) return;
   DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2 + 1], stream));
+  DLM_CALL(dlm_last_kernel_dims(prof_recs_[prof_next_].dims));
+  prof_recs_[prof_next_].kernel = dlm_last_kernel(1);
   ++prof_next_;
+}
+
+std::vector<UNet::KernelStats> UNet::profile_kernels(void* stream) {
+  DLM_CALL(dlm_stream_synchronize(stream));
+  std::vector<KernelStats> out;
+  std::map<std::string, size_t> at;
+  for (size_t i = 0; i < prof_next_ && i < prof_recs_.size(); ++i) {
+    float ms = 0.0f;
+    DLM_CALL(dlm_event_elapsed_ms(&ms, prof_events_[2 * i], prof_events_[2 * i + 1]));
+    const ProfRec& r = prof_recs_[i];
+    const std::string name = r.kernel.empty() ? "?" : r.kernel;
+    auto it = at.find(name);
+    if (it == at.end()) {
+      it = at.emplace(name, out.size()).first;
+      out.push_back(KernelStats{name, r.cls, 0, 0.0, 0.0, 0.0});
+    }
+    KernelStats& k = out[it->second];
+    k.count += 1;
+    k.ms += ms;
+    k.flops += r.flops;
+    k.bytes += r.bytes;
+    if (r.dims[0] > 0) ++k.dims[std::vector<int>(r.dims, r.dims + 4)];
+  }
+  return out;
 }
 
 std::vector<UNet::ClassStats> UNet::profile_report(void* stream) {
@@ -651,7 +684,9 @@ void UNet::conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, vo
   a.ldy = Co;
   const int Ho = (up ? 2 * H : (H + 2 - 3) / stride + 1), Wo = (up ? 2 * W : (W + 2 - 3) / stride + 1);
   const double cin = flop_cin > 0 ? flop_cin : (double)(C + Cb);
-  LAUNCH(kConv, 2.0 * B * Ho * Wo * Co * 9.0 * cin, 0.0, dlm_conv2d_nhwc_fp16(&a, stream));
+  LAUNCH(kConv, 2.0 * B * Ho * Wo * Co * 9.0 * cin,
+         2.0 * ((double)B * H * W * (C + Cb) + (double)Co * 9.0 * (C + Cb) + (double)B * Ho * Wo * Co),
+         dlm_conv2d_nhwc_fp16(&a, stream));
 }
 
 void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out,
@@ -685,7 +720,9 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
     a.tbias_ld = tproj_total_;
     a.out = h2;
     a.ldy = Co;
-    LAUNCH(kConv, 2.0 * B * HW * Co * 9.0 * Ci, 0.0, dlm_conv2d_nhwc_fp16(&a, stream));
+    LAUNCH(kConv, 2.0 * B * HW * Co * 9.0 * Ci,
+           2.0 * ((double)B * HW * Ci + (double)Co * 9.0 * Ci + (double)B * HW * Co),
+           dlm_conv2d_nhwc_fp16(&a, stream));
   }
   // norm2 + SiLU
   gn(h2, Co, nullptr, 0, r.n2g, r.n2b, h, B, HW, 1e-5f, true, stream);
@@ -720,7 +757,9 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
       a.residual = xa;
       a.res_ld = Co;
     }
-    LAUNCH(kConv, 2.0 * B * HW * Co * (9.0 * Co + (r.shortcut ? Ci : 0)), 0.0,
+    LAUNCH(kConv, 2.0 * B * HW * Co * (9.0 * Co + (r.shortcut ? Ci : 0)),
+           2.0 * ((double)B * HW * Co * 2.0 + (double)Co * (9.0 * Co + (r.shortcut ? Ci : 0)) +
+                  (double)B * HW * (r.shortcut ? Ci : Co)),
            dlm_conv2d_nhwc_fp16(&a, stream));
   }
 }
@@ -739,7 +778,7 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
   // self-attention
   LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
   // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
-  LAUNCH(kLinear, 2.0 * M * 3 * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * 3 * C * C, lin_bytes(M, 3 * C, C, 3 * C, false),
          dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, vt_ld, M,
                             3 * C, C, stream));
   {
@@ -768,12 +807,12 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
     LAUNCH(kAttention, 4.0 * B * heads * (double)HW * HW * 64, 0.0,
            dlm_attention_vt_fp16(&a, stream));
   }
-  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
        dlm_linear_fp16(o, C, k.wo1, C, k.bo1, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
                            stream));
   // cross-attention over the context's K / V^T (rows kv_off.. of stride kv_stride)
   LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln2g, k.ln2b, n, M, C, 1e-5f, stream));
-  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, false),
        dlm_linear_fp16(n, C, k.wq2, C, nullptr, nullptr, 0, qkv, C, M, C, C, 1.0f, 0.0f,
                            DLM_ACT_NONE, stream));
   {
@@ -804,15 +843,15 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
     LAUNCH(kAttention, 4.0 * B * heads * (double)HW * ctx_len * 64, 0.0,
            dlm_attention_vt_fp16(&a, stream));
   }
-  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
        dlm_linear_fp16(o, C, k.wo2, C, k.bo2, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
                            stream));
   // GEGLU feed-forward
   LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln3g, k.ln3b, n, M, C, 1e-5f, stream));
-  LAUNCH(kLinear, 2.0 * M * 8 * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * 8 * C * C, lin_bytes(M, 8 * C, C, 4 * C, false),
        dlm_linear_fp16(n, C, k.wff1, C, k.bff1, nullptr, 0, f, 4 * C, M, 8 * C, C, 1.0f,
                            0.0f, DLM_ACT_GEGLU, stream));
-  LAUNCH(kLinear, 2.0 * M * 4 * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * 4 * C * C, lin_bytes(M, C, 4 * C, C, true),
        dlm_linear_fp16(f, 4 * C, k.wff2, 4 * C, k.bff2, h, C, h, C, M, C, 4 * C, 1.0f, 1.0f,
                            DLM_ACT_NONE, stream));
 }
@@ -833,13 +872,13 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
   void* f = sc.alloc<uint16_t>((size_t)M * 4 * C);
 
   gn(x, C, nullptr, 0, t.ng, t.nb, g, B, HW, 1e-6f, false, stream);
-  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, false),
          dlm_linear_fp16(g, C, t.pin_w, C, t.pin_b, nullptr, 0, h, C, M, C, C, 1.0f, 0.0f,
                            DLM_ACT_NONE, stream));
   const TScratch ts{n, qkv, vt, vt_ld, o, f};
   for (const Block& k : t.blocks) tblock(k, C, h, ts, B, HW, kv, k.kv_off, kv_total_ / 2, ctx_len, stream);
   // proj_out + residual (the block input), written back in place
-  LAUNCH(kLinear, 2.0 * M * C * C, 0.0,
+  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
          dlm_linear_fp16(h, C, t.pout_w, C, t.pout_b, x, C, x, C, M, C, C, 1.0f, 1.0f,
                            DLM_ACT_NONE, stream));
 }
@@ -898,10 +937,10 @@ void UNet::run_transformer_block(const std::string& prefix, void* x, int B, int 
              ctx_pad};
   const char* kw = static_cast<const char*>(kv_w_) + (size_t)k.kv_off * cross * kH;
   const char* vw = static_cast<const char*>(kv_w_) + (size_t)(kv_half + k.kv_off) * cross * kH;
-  LAUNCH(kLinear, 2.0 * B * ctx_len * C * cross, 0.0,
+  LAUNCH(kLinear, 2.0 * B * ctx_len * C * cross, lin_bytes(B * ctx_len, C, cross, C, false),
          dlm_linear_fp16(ehs, cross, kw, cross, nullptr, nullptr, 0, kv.k, C, B * ctx_len, C, cross,
                          1.0f, 0.0f, DLM_ACT_NONE, stream));
-  LAUNCH(kLinear, 2.0 * B * ctx_len * C * cross, 0.0,
+  LAUNCH(kLinear, 2.0 * B * ctx_len * C * cross, lin_bytes(B * ctx_len, C, cross, C, false),
          dlm_linear_vt_fp16(ehs, cross, vw, cross, nullptr, kv.vt, 0, kv.vt, 0, ctx_len, ctx_pad,
                             B * ctx_len, C, cross, stream));
   const int vt_ld = (HW + 7) & ~7;
@@ -1002,7 +1041,8 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
   const int kv_half = kv_total_ / 2;
   const int ctx_pad = (ctx_len + 7) & ~7;
   CrossKV ckv{P((size_t)B * ctx_len * kv_half), P((size_t)B * kv_half * ctx_pad), ctx_pad};
-  LAUNCH(kLinear, 2.0 * B * ctx_len * kv_total_ * c.cross_dim, 0.0,
+  LAUNCH(kLinear, 2.0 * B * ctx_len * kv_total_ * c.cross_dim,
+         lin_bytes(B * ctx_len, kv_total_, c.cross_dim, kv_total_, false),
          dlm_linear_vt_fp16(ehs, c.cross_dim, kv_w_, c.cross_dim, nullptr, ckv.k, kv_half, ckv.vt,
                             kv_half, ctx_len, ctx_pad, B * ctx_len, kv_total_, c.cross_dim, stream));
 

@@ -135,6 +135,16 @@ class UNet {
     double ms = 0.0, flops = 0.0, bytes = 0.0;
   };
   std::vector<ClassStats> profile_report(void* stream);
+  // Same launches grouped by the kernel each one ran last (dlm_last_kernel):
+  // name -> class, launch count, kernel ms, algorithmic FLOPs and bytes.
+  struct KernelStats {
+    std::string name;
+    int cls = 0;
+    int count = 0;
+    double ms = 0.0, flops = 0.0, bytes = 0.0;
+    std::map<std::vector<int>, int> dims;  // GEMM problems (M, N, K, flags) -> launches
+  };
+  std::vector<KernelStats> profile_kernels(void* stream);
 
  private:
   struct Resnet {
@@ -248,6 +258,8 @@ class UNet {
   struct ProfRec {
     int cls;
     double flops, bytes;
+    std::string kernel;
+    int dims[4];
   };
   bool prof_on_ = false;
   std::vector<void*> prof_events_;

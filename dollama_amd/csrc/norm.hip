@@ -289,13 +289,13 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
   const size_t red_bytes = (size_t)p.R * C * sizeof(float2);
   if (red_bytes > 160 * 1024)
     return fail(DLM_ERR_UNSUPPORTED, "group_norm: channel count too large for one block");
-  hipLaunchKernelGGL(gn_partial_kernel<T>, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
+  DLM_LAUNCH("gn_partial_kernel", gn_partial_kernel<T>, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
                      ld_a, b, ld_b, HW, C, G, p.chunk, p.chunks, p.S, p.R, partial);
   DLM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
+  DLM_LAUNCH("gn_finalize_kernel", gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
                      p.chunks, (const f16*)gamma, (const f16*)beta, eps, ss);
   DLM_LAUNCH_CHECK();
-  hipLaunchKernelGGL(gn_apply_kernel<T>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a,
+  DLM_LAUNCH("gn_partial_kernel+gn_finalize_kernel+gn_apply_kernel", gn_apply_kernel<T>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a,
                      b, ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss, silu);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -414,15 +414,15 @@ int layer_norm(const void* in, const void* gamma, const void* beta, void* out, i
   const f16* b = (const f16*)beta;
   f16* y = (f16*)out;
   if (vec && C <= 64 * 8 * 1)
-    hipLaunchKernelGGL(layer_norm_kernel<1>, grid, block, 0, s, x, g, b, y, rows, C, eps);
+    DLM_LAUNCH("layer_norm_kernel<1>", layer_norm_kernel<1>, grid, block, 0, s, x, g, b, y, rows, C, eps);
   else if (vec && C <= 64 * 8 * 2)
-    hipLaunchKernelGGL(layer_norm_kernel<2>, grid, block, 0, s, x, g, b, y, rows, C, eps);
+    DLM_LAUNCH("layer_norm_kernel<2>", layer_norm_kernel<2>, grid, block, 0, s, x, g, b, y, rows, C, eps);
   else if (vec && C <= 64 * 8 * 3)
-    hipLaunchKernelGGL(layer_norm_kernel<3>, grid, block, 0, s, x, g, b, y, rows, C, eps);
+    DLM_LAUNCH("layer_norm_kernel<3>", layer_norm_kernel<3>, grid, block, 0, s, x, g, b, y, rows, C, eps);
   else if (vec && C <= 64 * 8 * 8)
-    hipLaunchKernelGGL(layer_norm_kernel<8>, grid, block, 0, s, x, g, b, y, rows, C, eps);
+    DLM_LAUNCH("layer_norm_kernel<8>", layer_norm_kernel<8>, grid, block, 0, s, x, g, b, y, rows, C, eps);
   else
-    hipLaunchKernelGGL(layer_norm_scalar_kernel, grid, block, 0, s, x, g, b, y, rows, C, eps);
+    DLM_LAUNCH("layer_norm_scalar_kernel", layer_norm_scalar_kernel, grid, block, 0, s, x, g, b, y, rows, C, eps);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

@@ -17,6 +17,20 @@
 namespace dlm {
 
 static thread_local std::string g_last_error;
+static thread_local const char* g_last_kernel = "";
+
+static thread_local int g_last_dims[4] = {0, 0, 0, 0};
+
+void note_kernel(const char* name) {
+  g_last_kernel = name ? name : "";
+  g_last_dims[0] = g_last_dims[1] = g_last_dims[2] = g_last_dims[3] = 0;
+}
+void note_dims(int M, int N, int K, int flags) {
+  g_last_dims[0] = M;
+  g_last_dims[1] = N;
+  g_last_dims[2] = K;
+  g_last_dims[3] = flags;
+}
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -83,6 +97,18 @@ extern "C" {
 const char* dlm_last_error(void) { return dlm::g_last_error.c_str(); }
 
 void dlm_set_last_error(const char* msg) { dlm::g_last_error = msg ? msg : ""; }
+
+const char* dlm_last_kernel(int reset) {
+  const char* k = dlm::g_last_kernel;
+  if (reset) dlm::note_kernel("");
+  return k;
+}
+
+int dlm_last_kernel_dims(int* dims) {
+  DLM_REQUIRE(dims != nullptr, "dims is NULL");
+  for (int i = 0; i < 4; ++i) dims[i] = dlm::g_last_dims[i];
+  return DLM_OK;
+}
 
 int dlm_get_device_count(int* count) {
   DLM_REQUIRE(count != nullptr, "count is NULL");

@@ -76,6 +76,7 @@ HOST_SIGNATURES = {
     "dlm_arena_stats": (I, [I, POINTER(c_uint64)]),
     "dlm_arena_fill": (I, [I, I]),
     "dlm_unet_run_resnet": (I, [P, ctypes.c_char_p, P, I, P, I, P, I, I, I, P, P]),
+    "dlm_unet_profile_kernels": (I, [P, ctypes.c_char_p, c_size_t, POINTER(c_size_t), P]),
     "dlm_unet_run_transformer_block": (I, [P, ctypes.c_char_p, P, I, I, P, I, P]),
     "dlm_arena_release": (I, [I]),
     "dlm_arena_reserve": (I, [I, c_size_t]),
@@ -275,8 +276,9 @@ class UNet:
         return out
 
     def _resnet_out_channels(self, prefix: str) -> int:
-        p = prefix.rstrip(".") + ".conv1.weight"
-        shape = dict(weight_specs(self.cfg)).get(p)
+        if getattr(self, "_specs", None) is None:
+            self._specs = weight_specs(self.cfg)
+        shape = self._specs.get(prefix.rstrip(".") + ".conv1.weight")
         if shape is None:
             raise KeyError(f"no resnet '{prefix}'")
         return shape[0]
@@ -349,6 +351,24 @@ class UNet:
         _call("dlm_unet_profile_report", self._h, v, _stream())
         return {c: {"launches": int(v[4 * i]), "ms": v[4 * i + 1], "flops": v[4 * i + 2],
                     "bytes": v[4 * i + 3]} for i, c in enumerate(self.KERNEL_CLASSES)}
+
+    def profile_kernels(self) -> dict:
+        """The last profiled forward by kernel instantiation: name -> {class,
+        launches, ms, flops, bytes}."""
+        need = c_size_t()
+        _call("dlm_unet_profile_kernels", self._h, None, 0, ctypes.byref(need), _stream())
+        buf = ctypes.create_string_buffer(need.value)
+        _call("dlm_unet_profile_kernels", self._h, buf, need.value, ctypes.byref(need), _stream())
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, cls, n, ms, fl, by, dims = line.split("\t")
+            problems = {}
+            for item in filter(None, dims.split(";")):
+                key, cnt = item.split(":")
+                problems[tuple(int(v) for v in key.split(","))] = int(cnt)
+            out[name] = {"class": self.KERNEL_CLASSES[int(cls)], "launches": int(n), "ms": float(ms),
+                         "flops": float(fl), "bytes": float(by), "problems": problems}
+        return out
 
     def set_stage_hook(self, fn: Optional[Callable[[str, int, int, int], None]]):
         """fn(name, device_ptr, n_elements, channels) after each stage."""

@@ -49,6 +49,15 @@ const char* dlm_last_error(void);
 /* Set this thread's error text (lets the C++ host layer report through the
  * same channel). */
 void dlm_set_last_error(const char* msg);
+/* Name of the kernel (template instantiation, as a profiler lists it) that
+ * the last entry point called on this thread launched last; "" if none since
+ * the last reset.  reset = 1 clears it after reading.  Lets a caller that
+ * times each call attribute the time to a kernel. */
+const char* dlm_last_kernel(int reset);
+/* Problem of that launch when it was a GEMM or implicit-GEMM conv: dims[0..3]
+ * = rows M, output columns N, reduction length K, flags (bit 0: residual
+ * epilogue; bits 4-7: activation code; bit 8: conv); zeros otherwise. */
+int dlm_last_kernel_dims(int* dims);
 int dlm_get_device_count(int* count);
 int dlm_set_device(int device);
 /* Name of the GPU architecture of the current device (e.g. "gfx950"). */

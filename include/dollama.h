@@ -143,6 +143,14 @@ int dlm_unet_graphs_captured(void* handle, size_t* count);
  * last forward run with profiling on.  Synchronises the stream. */
 int dlm_unet_set_profiling(void* handle, int on);
 int dlm_unet_profile_report(void* handle, double* out /* [24] */, void* stream);
+/* The last profiled forward grouped by kernel (the instantiation each launch
+ * ran last, dlm_last_kernel): one line per kernel, tab-separated
+ * "name class launches ms flops bytes dims", dims = "M,N,K,flags:launches;"
+ * for each GEMM problem the kernel ran (dlm_last_kernel_dims), in
+ * first-launch order.  *needed
+ * receives the text size including the terminating zero; buf (len bytes)
+ * may be NULL to query it. */
+int dlm_unet_profile_kernels(void* handle, char* buf, size_t len, size_t* needed, void* stream);
 
 /* Euler discrete scheduler (reference src/infer/scheduler.hpp:31-197:
  * scaled_linear betas 0.00085..0.012, leading spacing, steps_offset 1):
