@@ -844,7 +844,10 @@ __device__ __forceinline__ void split_coords(int bid, int tiles_m, int tiles_n, 
 // (already in registers) runs on the MFMA pipe; the whole ring is filled
 // before the loop and slot kt is refilled (with slice kt+NS) as soon as that
 // barrier proves every wave has read it.
-template <int BM, int BN, int WM, int WN, int NS, bool PF, class Desc>
+// SPS > 1: a ring stage holds SPS consecutive K slices published by one
+// barrier (fewer barriers and exposed first reads per slice); slices past the
+// range end are loaded clamped and skipped by the MFMAs.
+template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS, class Desc>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, SplitArgs sp) {
   constexpr int WAVES_N = BN / WN;
@@ -852,11 +855,13 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   constexpr int TM = WM / 16, TN = WN / 16;  // 16x16 MFMA blocks per wave
   constexpr int KS = BK / 32;                // 32-deep k-steps per slice
   constexpr int SA = BM * BK * 2;
-  constexpr int STAGE = (BM + BN) * BK * 2;
+  constexpr int SLICE = (BM + BN) * BK * 2;  // one K slice of both operands
+  constexpr int STAGE = SLICE * SPS;
   constexpr int GA = BM / 8, GB = BN / 8;    // 8-row DMA groups per operand tile
   constexpr int IA = (GA + NW - 1) / NW, IB = (GB + NW - 1) / NW;  // DMA instructions per wave
   static_assert(BM % 8 == 0 && BN % 8 == 0 && WM % 16 == 0 && WN % 16 == 0, "tile shape");
   static_assert(NS >= 2, "at least two slices");
+  static_assert(SPS == 1 || !PF, "multi-slice stages use the plain loop");
   __shared__ __attribute__((aligned(1024))) unsigned char smem_generic[NS * STAGE];
   unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_generic;
 
@@ -911,7 +916,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
     for (int i = 0; i < IB; ++i) dma_b(st, i, kt);
   };
 
-  constexpr int PRE = PF ? NS : NS - 1;  // slices in flight before the loop
+  constexpr int PRE = SPS > 1 ? 0 : (PF ? NS : NS - 1);  // slices in flight before the loop
 #pragma unroll
   for (int s = 0; s < PRE; ++s) issue_all(s, min(kb + s, ke - 1));
 
@@ -929,7 +934,68 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       DLM_WAIT_VM((P) * (IA + IB - 2));      \
     }                                        \
   } while (0)
-  if constexpr (PF) {
+  if constexpr (SPS > 1) {
+    static_assert(KS == 2, "multi-slice stages assume two k-steps per slice");
+    const int nsteps = (ke - kb + SPS - 1) / SPS;
+    auto slice_kt = [&](int t, int j) { return min(kb + t * SPS + j, ke - 1); };
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t)
+#pragma unroll
+      for (int j = 0; j < SPS; ++j) {
+        unsigned char DLM_LDS* dst = smem + t * STAGE + j * SLICE;
+        const int kt = slice_kt(t, j);
+        al.prepare(kt);
+#pragma unroll
+        for (int i = 0; i < IA; ++i) dma_a(dst, i, kt);
+#pragma unroll
+        for (int i = 0; i < IB; ++i) dma_b(dst, i, kt);
+      }
+    int slot = 0, nslot = NS - 1;  // stage being read, stage being refilled
+    for (int t = 0; t < nsteps; ++t) {
+      DLM_WAIT_SLICES((NS - 2) * SPS);  // stage t landed (this wave's part)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      const unsigned char DLM_LDS* st = smem + slot * STAGE;
+      unsigned char DLM_LDS* nst = smem + nslot * STAGE;
+      f16x8 fa[2][TM], fb[2][TN];
+      auto rd = [&](int q) {  // k-step q of the stage: slice q / KS, step q % KS
+        const unsigned char DLM_LDS* sl = st + (q / KS) * SLICE;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[q & 1][i] = frag(sl, wm * WM + i * 16 + (lane & 15), q % KS);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[q & 1][j] = frag(sl + SA, wn * WN + j * 16 + (lane & 15), q % KS);
+      };
+      rd(0);
+#pragma unroll
+      for (int q = 0; q < SPS * KS; ++q) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (q + 1 < SPS * KS) rd(q + 1);
+        // refill of stage t+NS-1: slice r's A rows at k-step 2r, its B rows at 2r+1
+        if ((q & 1) == 0) {
+          const int r = q >> 1;
+          const int kt = slice_kt(t + NS - 1, r);
+          al.prepare(kt);
+#pragma unroll
+          for (int i = 0; i < IA; ++i) dma_a(nst + r * SLICE, i, kt);
+        } else {
+          const int r = q >> 1;
+          const int kt = slice_kt(t + NS - 1, r);
+#pragma unroll
+          for (int i = 0; i < IB; ++i) dma_b(nst + r * SLICE, i, kt);
+        }
+        if (kb + t * SPS + q / KS < ke) {  // uniform: the last stage may end early
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(fb[q & 1][j], fa[q & 1][i], acc[i][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      slot = slot + 1 == NS ? 0 : slot + 1;
+      nslot = nslot + 1 == NS ? 0 : nslot + 1;
+    }
+  } else if constexpr (PF) {
     static_assert(KS == 2, "prefetch form assumes two k-steps per slice");
     f16x8 f0a[TM], f0b[TN], f1a[TM], f1b[TN];
     auto rd = [&](const unsigned char DLM_LDS* st, int ks, f16x8 (&fa)[TM], f16x8 (&fb)[TN]) {
@@ -972,6 +1038,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
+  int pslot = 0, pnslot = NS - 1;  // slot read this slice, slot refilled this slice
   for (int kt = kb; kt < ke; ++kt) {
     if (skips == 0) {
       DLM_WAIT_VM((NS - 2) * (IA + IB));
@@ -983,9 +1050,8 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    const int rel = kt - kb;
-    const unsigned char DLM_LDS* st = smem + (rel % NS) * STAGE;
-    unsigned char DLM_LDS* nst = smem + ((rel + NS - 1) % NS) * STAGE;
+    const unsigned char DLM_LDS* st = smem + pslot * STAGE;
+    unsigned char DLM_LDS* nst = smem + pnslot * STAGE;
     const int nkt = min(kt + NS - 1, ke - 1);
     al.prepare(nkt);
     f16x8 fa[2][TM], fb[2][TN];
@@ -1013,6 +1079,8 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    pslot = pslot + 1 == NS ? 0 : pslot + 1;
+    pnslot = pnslot + 1 == NS ? 0 : pnslot + 1;
   }
   }
 #undef DLM_WAIT_SLICES
@@ -1149,11 +1217,12 @@ struct NoSplitScope {
 
 // "dma_gemm_kernel<BM, BN, WM, WN, NS, PF, RowDesc|ConvDesc>", as the
 // profiler prints the instantiation
-template <int BM, int BN, int WM, int WN, int NS, bool PF, class Desc>
+template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS, class Desc>
 static const char* dma_kernel_name() {
   static const std::string n = "dma_gemm_kernel<" + std::to_string(BM) + ", " + std::to_string(BN) +
                                ", " + std::to_string(WM) + ", " + std::to_string(WN) + ", " +
                                std::to_string(NS) + ", " + (PF ? "true" : "false") + ", " +
+                               std::to_string(SPS) + ", " +
                                (std::is_same<Desc, RowDesc>::value ? "RowDesc" : "ConvDesc") + ">";
   return n.c_str();
 }
@@ -1166,10 +1235,10 @@ static const char* mfma_kernel_name() {
   return n.c_str();
 }
 
-template <int BM, int BN, int WM, int WN, int NS, bool PF = false, class Desc>
+template <int BM, int BN, int WM, int WN, int NS, bool PF = false, int SPS = 1, class Desc>
 static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
                       hipStream_t s, int S = 1) {
-  static_assert(NS * (BM + BN) * BK * 2 <= 160 * 1024, "LDS ring larger than 160 KiB");
+  static_assert(NS * SPS * (BM + BN) * BK * 2 <= 160 * 1024, "LDS ring larger than 160 KiB");
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
@@ -1186,9 +1255,9 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   }
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
   const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
-  note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, Desc>());
+  note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, Desc>());
   note_dims(M, N, bd.K, (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0));
-  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, Desc>), dim3(grid), dim3(NT), 0, s, ad,
+  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, Desc>), dim3(grid), dim3(NT), 0, s, ad,
                      bd, ep, tiles_m, tiles_n, sp);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -1297,6 +1366,11 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       case 32: return launch_dma<256, 128, 64, 64, 3, true>(ad, bd, ep, M, N, s);
       case 33: return launch_dma<128, 128, 64, 32, 4, true>(ad, bd, ep, M, N, s);
       case 34: return launch_dma<128, 64, 64, 32, 2, true>(ad, bd, ep, M, N, s);
+      case 35: return launch_dma<128, 80, 16, 80, 3, false, 2>(ad, bd, ep, M, N, s);
+      case 36: return launch_dma<128, 80, 16, 80, 2, false, 2>(ad, bd, ep, M, N, s);
+      case 37: return launch_dma<128, 160, 32, 80, 2, false, 2>(ad, bd, ep, M, N, s);
+      case 38: return launch_dma<128, 128, 64, 32, 2, false, 2>(ad, bd, ep, M, N, s);
+      case 39: return launch_dma<128, 64, 64, 32, 3, false, 2>(ad, bd, ep, M, N, s);
       default: break;
     }
     if (g_forced_tile == 0) {
@@ -1325,13 +1399,17 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       // 128x160 x2 splits from 44 slices, 256x160 x4 from 300.  Two splits of
       // a grid that already fills the chip measured slower than one or four.
       const int nk = (int)ceil_div(bd.K, BK);
-      // 2048-row outputs 1280 wide (one 1024-token level at B=2): 128x80
-      // tiles, 8 waves of 16x80, five-slice ring -> exactly 256 tiles
-      // (14.0 / 39.9 us at K = 1280 / 5120 against 15.1 / 43.9 for 128x128)
-      if (std::is_same<Desc, RowDesc>::value && !ep.vt && N % 80 == 0 &&
+      // 2048-row outputs 1280 wide (one 1024-token level at B=2) and the
+      // 8192x320 stride-2 conv: 128x80 tiles, 8 waves of 16x80 -> exactly
+      // 256 tiles.  Ring of three two-slice stages (one barrier per 128 of
+      // K): 15.5 / 40.3 us at K = 1280 / 5120 against 16.4 / 42.6 for a
+      // five-slice ring and 16.2 / 43.9 for 128x128; the conv 39.1 us
+      // against 47.3 for 128x160 x2 splits.  Convolutions with a long K
+      // (2048x1280x11520) stay on split 128x160 tiles.
+      if ((std::is_same<Desc, RowDesc>::value || nk <= 100) && !ep.vt && N % 80 == 0 &&
           ceil_div(M, 128) * (N / 80) >= kCUs * 3 / 4 &&
           ceil_div(M, 128) * (N / 80) <= kCUs && !(g_variant & 1))
-        return launch_dma<128, 80, 16, 80, 5>(ad, bd, ep, M, N, s);
+        return launch_dma<128, 80, 16, 80, 3, false, 2>(ad, bd, ep, M, N, s);
       if (!ep.vt && N % 160 == 0 && N <= 1280 && !(g_variant & 1)) {
         const long long t256 = ceil_div(M, 256) * (N / 160), t160 = ceil_div(M, 128) * (N / 160);
         if (t256 >= kCUs)
@@ -2008,7 +2086,7 @@ extern "C" int dlm_gemm_force_split(int splits) {
 }
 
 extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 34 && splits >= 0 && splits <= 64, "bad tile / split");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 39 && splits >= 0 && splits <= 64, "bad tile / split");
   if (M == 0 && N == 0 && K == 0) {
     dlm::g_overrides.clear();
     return DLM_OK;
@@ -2024,7 +2102,7 @@ extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int spl
 }
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 34, "tile_id must be in [0, 34]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 39, "tile_id must be in [0, 39]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

@@ -194,8 +194,10 @@ int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_pe
  * slice's first fragments read during the current slice's last MFMAs:
  * 27 128x80 16x80 5, 28 256x160 64x80 3, 29 128x128 64x32 2,
  * 30 128x160 32x80 4, 31 128x160 32x80 3, 32 256x128 64x64 3,
- * 33 128x128 64x32 4, 34 128x64 64x32 2.  Splits apply to the LDS-DMA core
- * only. */
+ * 33 128x128 64x32 4, 34 128x64 64x32 2; 35-39 ring stages of two K
+ * slices under one barrier (BMxBN, wave tile, stages): 35 128x80 16x80 3,
+ * 36 128x80 16x80 2, 37 128x160 32x80 2, 38 128x128 64x32 2,
+ * 39 128x64 64x32 3.  Splits apply to the LDS-DMA core only. */
 int dlm_gemm_force_tile(int tile_id);
 /* Same override for GEMMs / convs of one shape (M, N = output columns,
  * K = reduction length); tile 0 and splits 0 remove it, M = N = K = 0 clears

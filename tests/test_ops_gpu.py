@@ -55,15 +55,15 @@ def test_linear_geglu(gpu, M, d, K):
     assert_close(y, R.geglu(R.linear(x, w, b)), f"geglu {M}x{d}x{K}")
 
 
-@pytest.mark.parametrize("tile", list(range(8, 35)))
+@pytest.mark.parametrize("tile", list(range(8, 40)))
 def test_dma_tile_configs(gpu, tile):
-    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-34, the
-    fragment-prefetch forms 27-34 included), whole and split-K, on ragged
-    shapes with a K tail: bias + SiLU + residual, GEGLU, and a 3x3 conv with
-    residual."""
+    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-39, the
+    fragment-prefetch forms 27-34 and two-slice stages 35-39 included),
+    whole and split-K, on ragged shapes with an odd slice count and a K tail:
+    bias + SiLU + residual, GEGLU, and a 3x3 conv with residual."""
     from dollama_amd import _lib
     announce(f"forced DMA tile {tile}")
-    M, N, K = 300, 240, 712
+    M, N, K = 300, 240, 648  # 11 K slices: odd, with a tail
     x, w = randn((M, K), 13), randn((N, K), 14, std=0.04)
     b, r = randn((N,), 15, std=0.1), randn((M, N), 16)
     ref = R.silu(R.linear(x, w, b)) + r
