@@ -1381,12 +1381,13 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       // sit in lanes 16 apart, so any 16-column-multiple wave works).
       const long long t128 = ceil_div(M, 128) * ceil_div(N, 128);
       const bool pf = !(g_variant & 2);
-      // GEGLU FF1 (2048x10240 and 8192x5120, K 1280 / 640): 256x160 tiles,
-      // three-slice ring, measured in the whole UNet step in one process:
-      // 25.3 ms against 26.0 (128x128) and 26.7 (256x128); the fragment-
-      // prefetch form saves a further ~2 us (2048x10240) and ~12 us
-      // (8192x5120) per launch
-      if (ep.act == DLM_ACT_GEGLU && N % 160 == 0 && ceil_div(M, 256) * (N / 160) >= kCUs)
+      // GEGLU FF1 at 2048x10240x1280: 256x160 tiles, three-slice ring, with
+      // fragment prefetch, measured in the whole UNet step in one process
+      // (25.3 ms against 26.0 with 128x128 and 26.7 with 256x128 for both FF1
+      // shapes).  Grids of four or more 256x160 tiles per CU (8192x5120x640)
+      // take the 128x128 prefetch tiles below: 0.11 ms less per step.
+      if (ep.act == DLM_ACT_GEGLU && N % 160 == 0 && ceil_div(M, 256) * (N / 160) >= kCUs &&
+          ceil_div(M, 256) * (N / 160) < 4 * kCUs)
         return pf ? launch_dma<256, 160, 64, 80, 3, true>(ad, bd, ep, M, N, s)
                   : launch_dma<256, 160, 64, 80, 3>(ad, bd, ep, M, N, s);
       // Output widths that are multiples of 160 (SDXL's 320 / 640 / 1280

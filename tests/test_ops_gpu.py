@@ -258,6 +258,18 @@ def test_group_norm_large_offset(gpu):
     assert_close(ops.nhwc_to_nchw(y), ref, "group_norm large offset")
 
 
+def test_group_norm_many_samples(gpu):
+    """A batch of 4100 small samples: one statistics chunk per sample, one
+    merge wave per (sample, group)."""
+    N, C, H, W, G = 4100, 16, 3, 3, 4
+    announce("group_norm nhwc, N=4100")
+    x = randn((N, C, H, W), 87, std=1.5, mean=-0.5)
+    gm, bt = randn((C,), 88, std=0.3, mean=1.0), randn((C,), 89, std=0.3)
+    y = ops.group_norm_nhwc(ops.nchw_to_nhwc(to_gpu(x)), to_gpu(gm), to_gpu(bt), G, 1e-5, True)
+    ref = R.silu(R.group_norm(x, G, gm, bt, 1e-5))
+    assert_close(ops.nhwc_to_nchw(y), ref, "group_norm many samples")
+
+
 # ------------------------------------------------------------- LayerNorm ---
 @pytest.mark.parametrize("rows,C", [(8192, 640), (2048, 1280), (77, 2048), (5, 100)])
 def test_layer_norm(gpu, rows, C):
