@@ -129,7 +129,7 @@ struct ConvParams {
   int C0a, C0, ld0a, ld0b;
   int H, W;    // stored source resolution
   int Hv, Wv;  // resolution the taps index (2H x 2W when upsampling)
-  int KW, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, up;  // up: stride 1, dil 1 only
+  int KH, KW, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, up;  // up: stride 1, dil 1 only
   int K0;      // KH*KW*C0
   // segment 1: 1x1 conv over concat(src1a[:C1a], src1b[:C1-C1a]) at output res
   const f16* s1a;
@@ -176,9 +176,12 @@ struct ConvDesc : ConvParams {
         int kh, kw, ld, cc;
         bool kin = true;
         if (!d.generic) {
-          // one tap per K slice (C0 % 64 == 0): tap and channel are wave-uniform
-          const int tap = k0 / d.C0;
-          const int c = k0 - tap * d.C0;
+          // one tap per K slice (C0 % 64 == 0), channel blocks outermost:
+          // tap and channel are wave-uniform
+          const int taps = d.KH * d.KW;
+          const int cb = kt / taps;
+          const int tap = kt - cb * taps;
+          const int c = cb * BK;
           kh = tap / d.KW;
           kw = tap - kh * d.KW;
           const bool isa = c < d.C0a;
@@ -600,14 +603,14 @@ struct ConvDma {
   // uniform parameters
   const f16 *s0a, *s0b, *s1a, *s1b;
   unsigned bytes0a, bytes0b, bytes1a, bytes1b;
-  int C0, C0a, ld0a, ld0b, C1, C1a, ld1a, ld1b, K0, KW, Hv, Wv, W, up, M, dil_h, dil_w;
+  int C0, C0a, ld0a, ld0b, C1, C1a, ld1a, ld1b, K0, KH, KW, Hv, Wv, W, up, M, dil_h, dil_w;
   // per-slice state
   i32x4 rs;
   int seg, kh, kw, ld, cbase;
   __device__ ConvDma(const ConvParams& d, int m0, int nw, int wave, int lane)
       : s0a(d.s0a), s0b(d.s0b), s1a(d.s1a), s1b(d.s1b), bytes0a(d.bytes0a), bytes0b(d.bytes0b),
         bytes1a(d.bytes1a), bytes1b(d.bytes1b), C0(d.C0), C0a(d.C0a), ld0a(d.ld0a), ld0b(d.ld0b),
-        C1(d.C1), C1a(d.C1a), ld1a(d.ld1a), ld1b(d.ld1b), K0(d.K0), KW(d.KW), Hv(d.Hv), Wv(d.Wv),
+        C1(d.C1), C1a(d.C1a), ld1a(d.ld1a), ld1b(d.ld1b), K0(d.K0), KH(d.KH), KW(d.KW), Hv(d.Hv), Wv(d.Wv),
         W(d.W), up(d.up), M(d.M), dil_h(d.dil_h), dil_w(d.dil_w) {
 #pragma unroll
     for (int i = 0; i < I; ++i) {
@@ -625,28 +628,33 @@ struct ConvDma {
       iwb[i] = ow * d.stride_w - d.pad_w;
     }
   }
-  // Slices are requested in order (kb, kb+1, ..., then the last one
-  // repeated), so the tap / channel position advances by one slice at a
-  // time: no integer division and no branch in the loop (all selects).
+  // Segment-0 K order: 64-channel blocks outermost, then the taps (kh, kw),
+  // so the KH*KW slices that re-read one block of a pixel's channels run
+  // back to back and find its lines still in the L2.  Slices are requested
+  // in order (kb, kb+1, ..., then the last one repeated), so the tap /
+  // channel position advances by one slice at a time: no integer division
+  // and no branch in the loop (all selects).
   int cur_kt = 0, cur_c = 0, cur_kh = 0, cur_kw = 0;
   // position the tap state at slice kt (start of a split-K range)
   __device__ __forceinline__ void seek(int kt) {
-    const int k0 = kt * BK;
-    const int tap = k0 < K0 ? k0 / C0 : 0;
+    const int taps = KH * KW;
+    const bool s0 = kt * BK < K0;
+    const int cb = s0 ? kt / taps : 0;
+    const int tap = s0 ? kt - cb * taps : 0;
     cur_kt = kt;
-    cur_c = rfl(k0 < K0 ? k0 - tap * C0 : 0);
+    cur_c = rfl(cb * BK);
     cur_kh = rfl(tap / KW);
     cur_kw = rfl(tap - (tap / KW) * KW);
   }
   __device__ __forceinline__ void prepare(int kt) {
     const bool adv = kt != cur_kt;  // kt == cur_kt + 1
-    int c1 = cur_c + BK;
-    const bool wrap = c1 == C0;
-    c1 = wrap ? 0 : c1;
-    int kw1 = cur_kw + (wrap ? 1 : 0);
+    int kw1 = cur_kw + 1;
     const bool wrapw = kw1 == KW;
     kw1 = wrapw ? 0 : kw1;
-    const int kh1 = cur_kh + (wrapw ? 1 : 0);
+    int kh1 = cur_kh + (wrapw ? 1 : 0);
+    const bool wraph = kh1 == KH;
+    kh1 = wraph ? 0 : kh1;
+    const int c1 = cur_c + (wraph ? BK : 0);
     cur_c = rfl(adv ? c1 : cur_c);
     cur_kw = rfl(adv ? kw1 : cur_kw);
     cur_kh = rfl(adv ? kh1 : cur_kh);
@@ -1545,6 +1553,16 @@ __global__ void nhwc_to_nchw_kernel(const f16* __restrict__ in, f16* __restrict_
 }
 
 // out[co*ld + col0 + tap*Cin_pad + ci] = w[co][ci][tap] (zero for ci >= Cin)
+// Column of weight (tap, ci) within a packed conv segment of `taps` taps over
+// Cin_pad channels.  Cin_pad a multiple of 64 (the implicit-GEMM loaders'
+// one-tap-per-K-slice form): 64-channel blocks outermost, then taps, then
+// the block's channels, the K order those loaders walk; otherwise (the
+// small-channel form that decodes a tap per 8-channel vector) tap-major.
+__device__ __forceinline__ long long conv_wcol(int tap, int ci, int taps, int Cin_pad) {
+  if (Cin_pad % BK == 0) return ((long long)(ci / BK) * taps + tap) * BK + ci % BK;
+  return (long long)tap * Cin_pad + ci;
+}
+
 __global__ void conv_weight_pack_kernel(const f16* __restrict__ w, f16* __restrict__ out, int Cout,
                                         int Cin, int taps, int Cin_pad, int ld, int col0) {
   const long long total = (long long)Cout * taps * Cin_pad;
@@ -1555,12 +1573,12 @@ __global__ void conv_weight_pack_kernel(const f16* __restrict__ w, f16* __restri
     const int tap = (int)(r % taps);
     const int co = (int)(r / taps);
     const f16 v = ci < Cin ? w[((size_t)co * Cin + ci) * taps + tap] : (f16)0.0f;
-    out[(size_t)co * ld + col0 + (size_t)tap * Cin_pad + ci] = v;
+    out[(size_t)co * ld + col0 + conv_wcol(tap, ci, taps, Cin_pad)] = v;
   }
 }
 
-// out[co*ld + col0 + tap*Cin_pad + ci] += w[co][ci][tap] for ci < Cin (fp32
-// add, fp16 round); the zero padding ci >= Cin is left untouched.
+// out[co*ld + col0 + conv_wcol(tap, ci)] += w[co][ci][tap] for ci < Cin
+// (fp32 add, fp16 round); the zero padding ci >= Cin is left untouched.
 __global__ void conv_weight_pack_add_kernel(const f16* __restrict__ w, f16* __restrict__ out,
                                             int Cout, int Cin, int taps, int Cin_pad, int ld,
                                             int col0) {
@@ -1571,7 +1589,7 @@ __global__ void conv_weight_pack_add_kernel(const f16* __restrict__ w, f16* __re
     const long long r = idx / Cin;
     const int tap = (int)(r % taps);
     const int co = (int)(r / taps);
-    f16* o = out + (size_t)co * ld + col0 + (size_t)tap * Cin_pad + ci;
+    f16* o = out + (size_t)co * ld + col0 + conv_wcol(tap, ci, taps, Cin_pad);
     *o = (f16)((float)*o + (float)w[((size_t)co * Cin + ci) * taps + tap]);
   }
 }
@@ -1673,6 +1691,7 @@ int conv_nhwc_impl(const dlm_conv_nhwc_args* a, const ConvGeom& g, hipStream_t s
   d.W = a->W;
   d.Hv = Hv;
   d.Wv = Wv;
+  d.KH = a->KH;
   d.KW = a->KW;
   d.stride_h = g.sh;
   d.stride_w = g.sw;

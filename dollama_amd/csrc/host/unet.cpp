@@ -242,13 +242,16 @@ void UNet::read_weight(const std::string& key, void* host, size_t bytes, void* s
       const int src = s < 4 ? 4 * q + s : d + 4 * q + (s - 4);
       std::copy(raw.begin() + (size_t)r * K, raw.begin() + (size_t)(r + 1) * K, out + (size_t)src * K);
     }
-  } else {  // packed [co][col0 + tap * cin_pad + ci] <- [co][ci][tap]
+  } else {  // packed conv segment (dlm_conv_weight_pack_fp16's column order) <- [co][ci][tap]
     const int taps = pl.k * pl.k;
+    auto col = [&](int t, int ci) -> size_t {
+      if (pl.cin_pad % 64 == 0) return ((size_t)(ci / 64) * taps + t) * 64 + ci % 64;
+      return (size_t)t * pl.cin_pad + ci;
+    };
     for (int co = 0; co < pl.Co; ++co)
       for (int ci = 0; ci < pl.Ci; ++ci)
         for (int t = 0; t < taps; ++t)
-          out[((size_t)co * pl.Ci + ci) * taps + t] =
-              raw[(size_t)co * pl.ld + pl.col0 + (size_t)t * pl.cin_pad + ci];
+          out[((size_t)co * pl.Ci + ci) * taps + t] = raw[(size_t)co * pl.ld + pl.col0 + col(t, ci)];
   }
 }
 

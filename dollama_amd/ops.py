@@ -345,7 +345,8 @@ def pack_geglu(w: torch.Tensor, b: Optional[torch.Tensor]):
 
 
 def pack_conv_weight(w: torch.Tensor, cin_pad: Optional[int] = None, out=None, ld=None, col0=0):
-    """[Cout, Cin, KH, KW] -> [Cout, KH*KW*Cin_pad] channels-last per tap."""
+    """[Cout, Cin, KH, KW] -> [Cout, KH*KW*Cin_pad]: channel blocks of 64, then
+    taps, then channels when Cin_pad % 64 == 0, else taps then channels."""
     Cout, Cin, KH, KW = w.shape
     cp = cin_pad or Cin
     ld = ld or KH * KW * cp

@@ -265,8 +265,11 @@ int dlm_geglu_pack_fp16(const void* w, const void* bias, void* w_out, void* bias
                         int d, int K, void* stream);
 
 /* Repack a conv weight [Cout, Cin, KH, KW] into the channels-last GEMM form
- * [Cout, KH, KW, Cin_pad] (Cin_pad >= Cin, zero filled), written at row
- * stride ld_out elements (ld_out >= KH*KW*Cin_pad) starting at column col0. */
+ * (Cin_pad >= Cin, zero filled), written at row stride ld_out elements
+ * (ld_out >= KH*KW*Cin_pad) starting at column col0.  Column order: when
+ * Cin_pad is a multiple of 64, [Cin_pad/64][KH][KW][64] (channel blocks
+ * outermost, the K order the implicit-GEMM conv walks); otherwise
+ * [KH][KW][Cin_pad].  A 1x1 weight is [Cin_pad] either way. */
 int dlm_conv_weight_pack_fp16(const void* w, void* out, int Cout, int Cin, int KH, int KW,
                               int Cin_pad, int ld_out, int col0, void* stream);
 
@@ -294,8 +297,9 @@ int dlm_nhwc_to_nchw_fp16(const void* in, void* out, int N, int C, int HW, int C
  * Segment 1 (optional, C1a > 0) is a 1x1 stride-1 conv over the concatenation
  * of src1a/src1b at the output resolution, accumulated into the same sum
  * (the fused ResnetBlock2D conv_shortcut).  Weight rows are [Cout, Ktot] with
- * Ktot = KH*KW*(C0a+C0b) + (C1a+C1b), channels-last per tap (see
- * dlm_conv_weight_pack_fp16), row stride ldw.  Output channels-last with row
+ * Ktot = KH*KW*(C0a+C0b) + (C1a+C1b), segment 0 in the column order of
+ * dlm_conv_weight_pack_fp16 with Cin_pad = C0a+C0b, then segment 1, row
+ * stride ldw.  Output channels-last with row
  * stride ldy, or NCHW when out_nchw = 1; fp32 output elements when
  * out_f32 = 1 and an fp32 residual when res_f32 = 1 (the VAE decoder's fp32
  * stages, src/kernels/vae_decode.cu:317-327; operands stay fp16). */

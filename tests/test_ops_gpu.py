@@ -210,6 +210,24 @@ def test_conv_out_nchw_small_cout(gpu):
     assert_close(y, R.conv2d(x, w, b), "conv_out nchw")
 
 
+@pytest.mark.parametrize("Cin,cin_pad,k", [(128, 128, 3), (120, 128, 3), (72, 72, 3), (4, 8, 3), (320, 320, 1)])
+def test_conv_weight_pack_layout(gpu, Cin, cin_pad, k):
+    """dlm_conv_weight_pack_fp16's column order as include/dlm.h states it:
+    [Cin_pad/64][KH][KW][64] when Cin_pad % 64 == 0, else [KH][KW][Cin_pad];
+    zero padding channels."""
+    announce(f"conv weight pack Cin={Cin} pad={cin_pad} k={k}")
+    w = randn((16, Cin, k, k), 90)
+    got = ops.pack_conv_weight(to_gpu(w), cin_pad=cin_pad).float().cpu()
+    taps = k * k
+    wt = w.reshape(16, Cin, taps)
+    ref = torch.zeros(16, taps * cin_pad)
+    for ci in range(Cin):
+        for t in range(taps):
+            col = ((ci // 64) * taps + t) * 64 + ci % 64 if cin_pad % 64 == 0 else t * cin_pad + ci
+            ref[:, col] = wt[:, ci, t]
+    assert torch.equal(got, ref)
+
+
 # ------------------------------------------------------------- GroupNorm ---
 @pytest.mark.parametrize("N,C,H,W,G,eps,silu", [
     (2, 640, 64, 64, 32, 1e-5, True),
