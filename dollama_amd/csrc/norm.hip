@@ -7,10 +7,13 @@
 // variance at 0.  Here activations are channels-last [N, HW, C], so a pixel
 // row holds every group; the statistics are computed per channel over pixel
 // chunks with a per-chunk shift (first pixel of the chunk), which keeps the
-// fp32 partial sums well conditioned, and merged per group with Chan's
-// pairwise formula in fp64.  Three launches: partial statistics over
-// (chunk, n), a per-(n, group) merge producing per-channel scale/shift, and a
-// vectorised apply (+SiLU) pass.  Deterministic: fixed reduction order.
+// fp32 partial sums well conditioned; each block combines its channels into
+// per-group (mean, M2) with the equal-count form of Chan's formula, and the
+// chunks of one (n, group) are merged in fp64 by the two-pass decomposition
+// (mean first, then sum of M2_b + n_b (m_b - mean)^2).  Three launches:
+// partial statistics over (chunk, n), the per-(n, group) merge producing
+// per-channel scale/shift, and a vectorised apply (+SiLU) pass.
+// Deterministic: fixed reduction order.
 //
 // LayerNorm replaces launch_layer_norm (src/kernels/layernorm.cu:78-126):
 // one wave per row, the row held in registers, exact two-pass mean/variance.
