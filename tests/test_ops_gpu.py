@@ -364,11 +364,13 @@ def test_attention_strided_fused_qkv(gpu):
 
 @pytest.mark.parametrize("B,H,Sq,Sk", [(1, 1, 32, 64), (1, 2, 300, 136), (2, 10, 4096, 4096),
                                        (2, 20, 1024, 1024), (1, 3, 1000, 8), (2, 10, 4096, 77),
-                                       (2, 20, 1024, 77), (1, 2, 64, 5)])
+                                       (2, 20, 1024, 77), (1, 2, 64, 5), (1, 2, 70, 96), (2, 1, 40, 32),
+                                       (2, 1, 33, 1), (1, 2, 130, 97)])
 def test_attention_vt(gpu, B, H, Sq, Sk):
     """Flash attention over V^T [B, H, 64, Sk] with Q/K read from a fused
     [B, S, 2C] buffer; partial last key tiles, Sq not a multiple of the
-    query block, and both query-block widths are covered."""
+    query block, both query-block widths, and short key sets (one, two and three
+    32-key blocks, full and partial, Sk = 1) are covered."""
     Dh = 64
     C = H * Dh
     announce(f"attention_vt B={B} H={H} Sq={Sq} Sk={Sk}")
