@@ -252,6 +252,18 @@ def config_timings(net, U, dev, seed):
                                                  vt_strides=(H * 64 * S, 64 * S), vt_ld=S,
                                                  o_strides=(S * C, C, 64), scale=0.125))
         out[name] = entry(ms, 4.0 * B * H * S * S * 64)
+    # the reference-layout entry points a reference caller binds (NCHW conv with
+    # bias, [B, H, S, Dh] attention): layout conversions included
+    xn = rn(1, 320, 128, 128)
+    wn = rn(320, 320, 3, 3, std=0.02)
+    yn = torch.empty(1, 320, 128, 128, dtype=torch.float16, device=dev)
+    ms = time_calls(lambda: ops.launch_conv2d(xn, wn, b, yn, 1, 320, 128, 128, 320, 3, 3, 1, 1, 1, 1))
+    out["reference_layout_conv2d_nchw_320_128px_n1_bias"] = entry(ms, 2.0 * 16384 * 320 * 2880)
+    B, H, S = 2, 10, 4096
+    qa, ka, va = rn(B, H, S, 64), rn(B, H, S, 64), rn(B, H, S, 64)
+    oa = torch.empty(B, H, S, 64, dtype=torch.float16, device=dev)
+    ms = time_calls(lambda: ops.launch_attention(qa, ka, va, oa, B, H, S, S, 64, 0.125))
+    out["reference_layout_attention_b2_h10_s4096"] = entry(ms, 4.0 * B * H * S * S * 64)
     # 4: BasicTransformerBlock on 2x4096x640, context 2x77x2048 (incl. its K/V projections)
     xt = rn(2, 4096, 640)  # the block updates it in place on every call
     ctx = rn(2, 77, 2048)

@@ -7,9 +7,10 @@ widths on a small latent and at small widths with N = 2.  The fp32 stages
 are exercised with weights that push pre-residual sums past the fp16 range
 (the reason the reference keeps up blocks 2-3 in fp32,
 src/kernels/vae_decode.cu:9-19).  At the full 1024x1024 size (128x128
-latent, mid-block attention over S = 16384 pixels) the mid block is checked
-against a torch fp32 GPU reference, and the decode against itself (batch
-and repeat invariance).
+latent, mid-block attention over S = 16384 pixels) every stage and the final
+image are checked against the fp32 CPU oracle, the mid block against a torch
+fp32 GPU reference, and the decode against itself (batch and repeat
+invariance).
 """
 import ctypes
 import math
@@ -228,6 +229,30 @@ def test_vae_full_size_mid_block_and_invariance(gpu):
     assert torch.equal(img1, img2), "repeat decode differs"
     assert torch.equal(img3[0], img1[0]) and torch.equal(img3[1], img1[0]), "N=2 decode != N=1"
     net.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.slow
+def test_vae_full_size_decode_parity(gpu):
+    """The whole 1024x1024 decode (128x128 latent, SDXL widths, mid-block
+    attention over 16384 pixels) against the fp32 CPU oracle: every golden
+    stage and the final image (the reference gates its final image on SSIM,
+    src/tests/test_vae_decode.cu)."""
+    print("[case] SDXL VAE 128x128 latent -> 1024x1024 vs fp32 CPU oracle", flush=True)
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    W = OV.random_weights(OV.SDXL_VAE, seed=51)
+    lat = _latent(1, 128, 128, seed=52)
+    stages = {}
+    got = _decode_gpu(V.SDXL_VAE_CONFIG, W, lat, stages)
+    torch.cuda.empty_cache()
+    stages_ref = {}
+    with torch.no_grad():
+        ref = OV.vae_decode(W, OV.SDXL_VAE, lat, stages_ref)
+    _check_stages(stages, stages_ref, "sdxl 1024x1024")
+    assert_close(got, ref, "sdxl 1024x1024 final_image")
+    s = metrics.ssim_uniform(got, ref)
+    print(f"[parity] sdxl 1024x1024 final_image SSIM={s:.7f}", flush=True)
+    assert s >= 0.9999
 
 
 @pytest.mark.gpu
