@@ -806,6 +806,140 @@ __device__ __forceinline__ void epi4_geglu(const f32x4& a, int row, int col, con
   *reinterpret_cast<uint32_t*>(ep.y + (size_t)row * ep.ldy + ocol) = *reinterpret_cast<uint32_t*>(o2);
 }
 
+// Whole-tile epilogues of a wave's TM x TN blocks (lane: row (lane & 15) of
+// block i, columns 4 (lane >> 4) + [0, 4) of block j) for fp16 row-major
+// output.  Every bias / time-bias / residual load is issued before the first
+// use, at addresses clamped into the tensors, so the wave waits on memory
+// once; per block, the loads, guards and stores of epi4 (one round trip per
+// operand and block) made the epilogue several times longer.  The arithmetic
+// is epi4's, in the same order.
+__device__ __forceinline__ bool epi_tile_fast(const EpiArgs& ep) {
+  return !ep.y_f32 && !ep.res_f32 && !ep.out_nchw && !ep.vt;
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, int col0, const EpiArgs& ep) {
+  f16x4 bv[TN], tv[TM][TN], rv[TM][TN];
+  if (ep.bias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bv[j] = ld4h(ep.bias + min(col0 + j * 16, ep.N - 4));
+  }
+  if (ep.tbias) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = min(row0 + i * 16, ep.M - 1);
+      const int n = ep.rows_per_sample > 0 ? r / ep.rows_per_sample : 0;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) tv[i][j] = ld4h(ep.tbias + (size_t)n * ep.tbias_ld + min(col0 + j * 16, ep.N - 4));
+    }
+  }
+  if (ep.res) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = min(row0 + i * 16, ep.M - 1);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) rv[i][j] = ld4h(ep.res + (size_t)r * ep.ldr + min(col0 + j * 16, ep.N - 4));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = row0 + i * 16;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = col0 + j * 16;
+      float v[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = acc[i][j][t] * ep.alpha;
+      if (ep.bias) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] += (float)bv[j][t];
+      }
+      if (ep.tbias) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] += (float)tv[i][j][t];
+      }
+      if (ep.act == DLM_ACT_SILU) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = silu_f(v[t]);
+      } else if (ep.act == DLM_ACT_GELU) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = gelu_erf_f(v[t]);
+      }
+      if (ep.res) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)rv[i][j][t];
+      }
+      if (row < ep.M && col < ep.N) {
+        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        *reinterpret_cast<f16x4*>(ep.y + (size_t)row * ep.ldy + col) = o;
+      }
+    }
+  }
+}
+
+// GEGLU form of epi_tile (see epi4_geglu for the lane pairing).
+template <int TM, int TN>
+__device__ __forceinline__ void epi_tile_geglu(const f32x4 (&acc)[TM][TN], int row0, int col0,
+                                               const EpiArgs& ep) {
+  const bool is_gate = (col0 & 4) != 0;
+  const int t0 = is_gate ? 2 : 0;
+  f16x2 bvv[TN], bgg[TN], rv[TM][TN];
+  if (ep.bias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int vc = min((col0 + j * 16) & ~4, ep.N - 8);
+      bvv[j] = *reinterpret_cast<const f16x2*>(ep.bias + vc + t0);
+      bgg[j] = *reinterpret_cast<const f16x2*>(ep.bias + vc + 4 + t0);
+    }
+  }
+  if (ep.res) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = min(row0 + i * 16, ep.M - 1);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int oc = (min((col0 + j * 16) & ~4, ep.N - 8) >> 1) + t0;
+        rv[i][j] = *reinterpret_cast<const f16x2*>(ep.res + (size_t)r * ep.ldr + oc);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = row0 + i * 16;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const f32x4& a = acc[i][j];
+      // value lane sends values 2-3, gate lane sends gates 0-1
+      const float r0 = __shfl_xor(is_gate ? a[0] : a[2], 16, 64);
+      const float r1 = __shfl_xor(is_gate ? a[1] : a[3], 16, 64);
+      const int vcol = (col0 + j * 16) & ~4;
+      float v[2], g[2];
+      v[0] = (is_gate ? r0 : a[0]) * ep.alpha;
+      v[1] = (is_gate ? r1 : a[1]) * ep.alpha;
+      g[0] = (is_gate ? a[2] : r0) * ep.alpha;
+      g[1] = (is_gate ? a[3] : r1) * ep.alpha;
+      if (ep.bias) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          v[t] += (float)bvv[j][t];
+          g[t] += (float)bgg[j][t];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) v[t] *= gelu_erf_fast(g[t]);
+      if (ep.res) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) v[t] += ep.beta * (float)rv[i][j][t];
+      }
+      if (row < ep.M && vcol < ep.N) {
+        f16 o2[2] = {(f16)v[0], (f16)v[1]};
+        *reinterpret_cast<uint32_t*>(ep.y + (size_t)row * ep.ldy + (vcol >> 1) + t0) =
+            *reinterpret_cast<uint32_t*>(o2);
+      }
+    }
+  }
+}
+
 // Split-K: the K slices of a tile are divided into S ranges of kps slices,
 // one workgroup each.  Every split stores its fp32 accumulators (agent-scope
 // stores, so the data is visible device-wide once the store is counted
@@ -1159,6 +1293,18 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   // block i and output columns 4 (lane >> 4) + [0, 4) of block j.
   const int row0 = m0 + wm * WM + (lane & 15);
   const int col0 = n0 + wn * WN + 4 * (lane >> 4);
+  // the batched forms hold every loaded operand in registers: wave tiles of
+  // up to 20 blocks (the largest wave tile, 128x64, keeps the per-block form)
+  if constexpr (TM * TN <= 20) {
+    if (ep.act == DLM_ACT_GEGLU) {
+      epi_tile_geglu<TM, TN>(acc, row0, col0, ep);
+      return;
+    }
+    if (epi_tile_fast(ep)) {
+      epi_tile<TM, TN>(acc, row0, col0, ep);
+      return;
+    }
+  }
   if (ep.act == DLM_ACT_GEGLU) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
