@@ -817,10 +817,31 @@ __device__ __forceinline__ bool epi_tile_fast(const EpiArgs& ep) {
   return !ep.y_f32 && !ep.res_f32 && !ep.out_nchw && !ep.vt;
 }
 
+// Bias and residual of the wave tile, loaded unconditionally (a missing
+// operand reads the output tile instead, never used): exactly TN + TM TN
+// loads, so a K loop that issues them before its last waits can count them.
 template <int TM, int TN>
-__device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, int col0, const EpiArgs& ep) {
-  f16x4 bv[TN], tv[TM][TN], rv[TM][TN];
-  if (ep.bias) {
+__device__ __forceinline__ void epi_tile_early(int row0, int col0, const EpiArgs& ep, f16x4 (&bv)[TN],
+                                               f16x4 (&rv)[TM][TN]) {
+  const f16* bp = ep.bias ? ep.bias : ep.y;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bv[j] = ld4h(bp + min(col0 + j * 16, ep.N - 4));
+  const f16* rp = ep.res ? ep.res : ep.y;
+  const int ld = ep.res ? ep.ldr : ep.ldy;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = min(row0 + i * 16, ep.M - 1);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) rv[i][j] = ld4h(rp + (size_t)r * ld + min(col0 + j * 16, ep.N - 4));
+  }
+}
+
+// EARLY: bias and residual already in bv / rv (epi_tile_early).
+template <int TM, int TN, bool EARLY = false>
+__device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, int col0, const EpiArgs& ep,
+                                         f16x4 (&bv)[TN], f16x4 (&rv)[TM][TN]) {
+  f16x4 tv[TM][TN];
+  if (!EARLY && ep.bias) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) bv[j] = ld4h(ep.bias + min(col0 + j * 16, ep.N - 4));
   }
@@ -833,7 +854,7 @@ __device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, i
       for (int j = 0; j < TN; ++j) tv[i][j] = ld4h(ep.tbias + (size_t)n * ep.tbias_ld + min(col0 + j * 16, ep.N - 4));
     }
   }
-  if (ep.res) {
+  if (!EARLY && ep.res) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int r = min(row0 + i * 16, ep.M - 1);
@@ -1058,6 +1079,15 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
     for (int i = 0; i < IB; ++i) dma_b(st, i, kt);
   };
 
+  // Early epilogue loads (two-slice-stage loop, residual linears): the bias
+  // and residual of the wave tile are requested once the last real refill
+  // is issued, so their latency passes under the last stages' MFMAs; the
+  // refills past the end are then skipped and the tail's waits count them.
+  const int erow0 = m0 + wm * WM + (lane & 15);
+  const int ecol0 = n0 + wn * WN + 4 * (lane >> 4);
+  f16x4 ebv[TN], erv[TM][TN];
+  bool early = false;
+
   constexpr int PRE = SPS > 1 ? 0 : (PF ? NS : NS - 1);  // slices in flight before the loop
 #pragma unroll
   for (int s = 0; s < PRE; ++s) issue_all(s, min(kb + s, ke - 1));
@@ -1076,6 +1106,17 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       DLM_WAIT_VM((P) * (IA + IB - 2));      \
     }                                        \
   } while (0)
+  // P slices of DMA plus E other loads may still be outstanding
+#define DLM_WAIT_SLICES_PLUS(P, E)                \
+  do {                                            \
+    if (skips == 0) {                             \
+      DLM_WAIT_VM((P) * (IA + IB) + (E));         \
+    } else if (skips == 1) {                      \
+      DLM_WAIT_VM((P) * (IA + IB - 1) + (E));     \
+    } else {                                      \
+      DLM_WAIT_VM((P) * (IA + IB - 2) + (E));     \
+    }                                             \
+  } while (0)
   if constexpr (SPS > 1) {
     static_assert(KS == 2, "multi-slice stages assume two k-steps per slice");
     const int nsteps = (ke - kb + SPS - 1) / SPS;
@@ -1092,12 +1133,30 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
 #pragma unroll
         for (int i = 0; i < IB; ++i) dma_b(dst, i, kt);
       }
+    // t_e: first stage whose refill would lie past the end (every real
+    // stage's DMA is issued before it)
+    const int t_e = nsteps - (NS - 1);
+    if constexpr (TM * TN <= 20)
+      early = sp.S == 1 && t_e >= 1 && ep.res && !ep.tbias && ep.act != DLM_ACT_GEGLU && epi_tile_fast(ep);
     int slot = 0, nslot = NS - 1;  // stage being read, stage being refilled
     for (int t = 0; t < nsteps; ++t) {
-      DLM_WAIT_SLICES((NS - 2) * SPS);  // stage t landed (this wave's part)
+      if (early && t > t_e) {
+        // newer than stage t: the DMA of stages t+1 .. nsteps-1 and the
+        // TN + TM TN early loads
+        static_assert(NS <= 4, "tail waits written out for rings of up to four stages");
+        if (nsteps - 1 - t == 0) {
+          DLM_WAIT_SLICES_PLUS(0, TN + TM * TN);
+        } else {
+          DLM_WAIT_SLICES_PLUS(SPS, TN + TM * TN);
+        }
+      } else {
+        DLM_WAIT_SLICES((NS - 2) * SPS);  // stage t landed (this wave's part)
+      }
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
+      if (early && t == t_e) epi_tile_early<TM, TN>(erow0, ecol0, ep, ebv, erv);
+      const bool refill = !early || t < t_e;
       const unsigned char DLM_LDS* st = smem + slot * STAGE;
       unsigned char DLM_LDS* nst = smem + nslot * STAGE;
       f16x8 fa[2][TM], fb[2][TN];
@@ -1114,7 +1173,8 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
         __builtin_amdgcn_sched_barrier(0);
         if (q + 1 < SPS * KS) rd(q + 1);
         // refill of stage t+NS-1: slice r's A rows at k-step 2r, its B rows at 2r+1
-        if ((q & 1) == 0) {
+        if (!refill) {
+        } else if ((q & 1) == 0) {
           const int r = q >> 1;
           const int kt = slice_kt(t + NS - 1, r);
           al.prepare(kt);
@@ -1226,6 +1286,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   }
   }
 #undef DLM_WAIT_SLICES
+#undef DLM_WAIT_SLICES_PLUS
   DLM_WAIT_VM(0);  // no DMA may still be writing this workgroup's LDS at exit
 
   if (sp.S > 1) {
@@ -1301,7 +1362,12 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       return;
     }
     if (epi_tile_fast(ep)) {
-      epi_tile<TM, TN>(acc, row0, col0, ep);
+      if (early) {
+        epi_tile<TM, TN, true>(acc, row0, col0, ep, ebv, erv);
+      } else {
+        f16x4 bv[TN], rv[TM][TN];
+        epi_tile<TM, TN>(acc, row0, col0, ep, bv, rv);
+      }
       return;
     }
   }
