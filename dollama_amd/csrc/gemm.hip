@@ -898,8 +898,15 @@ __device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, i
   }
 }
 
-// GEGLU form of epi_tile (see epi4_geglu for the lane pairing).
-template <int TM, int TN>
+// GEGLU form of epi_tile.  The value lanes of a pair (see epi4_geglu) are
+// the even 16-lane rows of the wave (packed column 4 (lane >> 4) of a block
+// is a value column when lane >> 4 is even, since tile and block origins are
+// multiples of 16), the gate lanes the odd rows; one v_permlane16_swap per
+// accumulator pair (0, 2) and (1, 3) leaves every lane holding the values and
+// gates of its own two output columns, with no select and no LDS traffic.
+// FULL: the wave tile lies inside M x N, so no store needs a guard and the
+// blocks' independent GELU chains can interleave.
+template <int TM, int TN, bool FULL>
 __device__ __forceinline__ void epi_tile_geglu(const f32x4 (&acc)[TM][TN], int row0, int col0,
                                                const EpiArgs& ep) {
   const bool is_gate = (col0 & 4) != 0;
@@ -930,15 +937,14 @@ __device__ __forceinline__ void epi_tile_geglu(const f32x4 (&acc)[TM][TN], int r
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const f32x4& a = acc[i][j];
-      // value lane sends values 2-3, gate lane sends gates 0-1
-      const float r0 = __shfl_xor(is_gate ? a[0] : a[2], 16, 64);
-      const float r1 = __shfl_xor(is_gate ? a[1] : a[3], 16, 64);
+      const auto s02 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[0]), __float_as_uint(a[2]), false, false);
+      const auto s13 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[1]), __float_as_uint(a[3]), false, false);
       const int vcol = (col0 + j * 16) & ~4;
       float v[2], g[2];
-      v[0] = (is_gate ? r0 : a[0]) * ep.alpha;
-      v[1] = (is_gate ? r1 : a[1]) * ep.alpha;
-      g[0] = (is_gate ? a[2] : r0) * ep.alpha;
-      g[1] = (is_gate ? a[3] : r1) * ep.alpha;
+      v[0] = __uint_as_float(s02[0]) * ep.alpha;
+      v[1] = __uint_as_float(s13[0]) * ep.alpha;
+      g[0] = __uint_as_float(s02[1]) * ep.alpha;
+      g[1] = __uint_as_float(s13[1]) * ep.alpha;
       if (ep.bias) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -952,11 +958,9 @@ __device__ __forceinline__ void epi_tile_geglu(const f32x4 (&acc)[TM][TN], int r
 #pragma unroll
         for (int t = 0; t < 2; ++t) v[t] += ep.beta * (float)rv[i][j][t];
       }
-      if (row < ep.M && vcol < ep.N) {
-        f16 o2[2] = {(f16)v[0], (f16)v[1]};
-        *reinterpret_cast<uint32_t*>(ep.y + (size_t)row * ep.ldy + (vcol >> 1) + t0) =
-            *reinterpret_cast<uint32_t*>(o2);
-      }
+      f16 o2[2] = {(f16)v[0], (f16)v[1]};
+      uint32_t* dst = reinterpret_cast<uint32_t*>(ep.y + (size_t)row * ep.ldy + (vcol >> 1) + t0);
+      if (FULL || (row < ep.M && vcol < ep.N)) *dst = *reinterpret_cast<uint32_t*>(o2);
     }
   }
 }
@@ -1358,7 +1362,11 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   // up to 20 blocks (the largest wave tile, 128x64, keeps the per-block form)
   if constexpr (TM * TN <= 20) {
     if (ep.act == DLM_ACT_GEGLU) {
-      epi_tile_geglu<TM, TN>(acc, row0, col0, ep);
+      if (m0 + BM <= ep.M && n0 + BN <= ep.N) {
+        epi_tile_geglu<TM, TN, true>(acc, row0, col0, ep);
+      } else {
+        epi_tile_geglu<TM, TN, false>(acc, row0, col0, ep);
+      }
       return;
     }
     if (epi_tile_fast(ep)) {
