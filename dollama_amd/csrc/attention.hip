@@ -478,20 +478,34 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   }
   FA_WAIT_VM(0);
 
-  const int qi = q0 + (lane & 31);
+  // O leaves through LDS: a lane holds 8-byte pieces of one query row, so
+  // direct stores would write 32 rows in 16-byte fragments per instruction;
+  // staged, every store instruction writes four whole 128-byte head rows.
+  // When every workgroup ends together (two-tile cross attention) the
+  // fragment stores took several microseconds of the launch.
+  const int ql = lane & 31;
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / l_tot;
-  if (qi < p.Sq) {
-    f16* obase = p.o + b * p.o_sb + h * p.o_sh + (long long)qi * p.o_ss;
+  __syncthreads();  // every wave is done reading the K / V^T ring
+  unsigned char DLM_LDS* ob = smem + wave * 4096;  // this wave's 32 rows x 128 B, chunks swizzled
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        f16x4 r;
+    for (int gq = 0; gq < 4; ++gq) {
+      f16x4 r;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) r[t] = (f16)(o[dt][4 * gq + t] * inv);
-        *reinterpret_cast<f16x4*>(obase + dt * 32 + 8 * gq + 4 * g) = r;
-      }
+      for (int t = 0; t < 4; ++t) r[t] = (f16)(o[dt][4 * gq + t] * inv);
+      const int chunk = dt * 4 + gq;
+      *reinterpret_cast<f16x4 DLM_LDS*>(ob + ql * 128 + ((chunk ^ (ql & 7)) * 16) + g * 8) = r;
+    }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = i * 4 + (lane >> 4), piece = lane & 15;
+    const f16x4 r = *reinterpret_cast<const f16x4 DLM_LDS*>(ob + row * 128 + (((piece >> 1) ^ (row & 7)) * 16) +
+                                                             (piece & 1) * 8);
+    const int qi = q0 + row;
+    if (qi < p.Sq)
+      *reinterpret_cast<f16x4*>(p.o + b * p.o_sb + h * p.o_sh + (long long)qi * p.o_ss + piece * 4) = r;
   }
 }
 
