@@ -115,6 +115,9 @@ HIP_SIGNATURES = {
     "dlm_attention_strided_fp16": (I, [POINTER(AttentionArgs), P]),
     "dlm_attention_vt_fp16": (I, [POINTER(AttentionVtArgs), P]),
     "dlm_linear_vt_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, I, I, P]),
+    "dlm_linear_ln_fp16": (I, [P, I, P, I, P, P, F, P, I, P, I, I, I, I, F, I, P]),
+    "dlm_linear_vt_ln_fp16": (I, [P, I, P, I, P, P, F, P, I, P, I, I, I, I, I, I, P]),
+    "dlm_ln_fold_fp16": (I, [P, I, I, I, P, P, P, P, I, P, P, P]),
     "dlm_sdxl_embed_inputs_fp16": (I, [P, P, I, P, I, I, P, I, P, I, P]),
     "dlm_linear_small_fp16": (I, [P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),

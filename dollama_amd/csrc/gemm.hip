@@ -61,6 +61,15 @@ struct EpiArgs {
   // fp16 range, attention scores ahead of a softmax)
   int y_f32;
   int res_f32;
+  // LayerNorm folded into the GEMM (LNS kernels): A holds the raw rows x, W
+  // the weight with gamma folded into its K columns; the epilogue forms
+  // rstd * acc - rstd * mean * ln_c1[col] + ln_c2[col] with the row's
+  // statistics accumulated in the K loop (mean = sum x / K,
+  // var = max(sum x^2 / K - mean^2, 0), rstd = 1 / sqrt(var + ln_eps))
+  const float* ln_c1;
+  const float* ln_c2;
+  float ln_invk;
+  float ln_eps;
 };
 
 // ---------------------------------------------------------------------------
@@ -701,6 +710,16 @@ struct DmaOf<ConvDesc> {
 
 __device__ __forceinline__ f16x4 ld4h(const f16* p) { return *reinterpret_cast<const f16x4*>(p); }
 
+// LayerNorm fold of four accumulators of columns [col, col+4): r = rstd,
+// rm = rstd * mean of the row, c1 / c2 the columns' ln_c1 / ln_c2.
+__device__ __forceinline__ f32x4 ln_fold4(const f32x4& a, const f32x4& c1, const f32x4& c2, float r,
+                                         float rm) {
+  f32x4 o;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = __builtin_fmaf(a[t], r, __builtin_fmaf(-rm, c1[t], c2[t]));
+  return o;
+}
+
 // Epilogue of four consecutive output columns [col, col+4) of one row.
 __device__ __forceinline__ void epi4(const f32x4& a, int row, int col, const EpiArgs& ep) {
   if (row >= ep.M || col >= ep.N) return;
@@ -1014,7 +1033,11 @@ __device__ __forceinline__ void split_coords(int bid, int tiles_m, int tiles_n, 
 // SPS > 1: a ring stage holds SPS consecutive K slices published by one
 // barrier (fewer barriers and exposed first reads per slice); slices past the
 // range end are loaded clamped and skipped by the MFMAs.
-template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS, class Desc>
+// LNS: LayerNorm folded in (EpiArgs::ln_*): every wave sums x and x^2 of its
+// rows from the A fragments it multiplies (two v_dot2 per 4 halves, fp32
+// accumulation of exact fp16 products); the four lanes that hold one row's
+// K chunks combine their sums after the loop.  No split-K.
+template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS, bool LNS, class Desc>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, SplitArgs sp) {
   constexpr int WAVES_N = BN / WN;
@@ -1057,6 +1080,23 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float ln_s1[LNS ? TM : 1], ln_s2[LNS ? TM : 1];
+#pragma unroll
+  for (int i = 0; i < (LNS ? TM : 1); ++i) ln_s1[i] = ln_s2[i] = 0.0f;
+  // row sums of x and x^2 over one k-step's A fragments
+  auto ln_acc = [&](const f16x8* fa) {
+    if constexpr (LNS) {
+      const f16x2 one2 = f16x2{(f16)1.0f, (f16)1.0f};
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const f16x2 x2 = f16x2{fa[i][2 * h], fa[i][2 * h + 1]};
+          ln_s1[i] = __builtin_amdgcn_fdot2(x2, one2, ln_s1[i], false);
+          ln_s2[i] = __builtin_amdgcn_fdot2(x2, x2, ln_s2[i], false);
+        }
+    }
+  };
 
   // 16-row operand fragment of k-step ks: lane holds row (lane & 15), k
   // chunk 4 ks + (lane >> 4) (the 16x16x32 MFMA operand layout).
@@ -1195,6 +1235,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
           for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(fb[q & 1][j], fa[q & 1][i], acc[i][j]);
+          ln_acc(fa[q & 1]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1215,6 +1256,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(fb[j], fa[i], acc[i][j]);
+      ln_acc(fa);
     };
     DLM_WAIT_SLICES(NS - 1);  // slice kb
     __builtin_amdgcn_s_barrier();
@@ -1283,6 +1325,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
+      ln_acc(fa[ks & 1]);
       __builtin_amdgcn_sched_barrier(0);
     }
     pslot = pslot + 1 == NS ? 0 : pslot + 1;
@@ -1293,7 +1336,7 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
 #undef DLM_WAIT_SLICES_PLUS
   DLM_WAIT_VM(0);  // no DMA may still be writing this workgroup's LDS at exit
 
-  if (sp.S > 1) {
+  if (!LNS && sp.S > 1) {
     // ---- split-K reduction (last arriver) ----
     const int tile = tmi * tiles_n + tni;
     constexpr int PER = BM * BN;  // floats per partial
@@ -1358,6 +1401,32 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
   // block i and output columns 4 (lane >> 4) + [0, 4) of block j.
   const int row0 = m0 + wm * WM + (lane & 15);
   const int col0 = n0 + wn * WN + 4 * (lane >> 4);
+  if constexpr (LNS) {
+    // LayerNorm fold: rstd and rstd * mean of each row from the x and x^2
+    // sums (lanes l, l^16, l^32, l^48 hold the four K chunks of row l & 15),
+    // the columns' ln_c1 / ln_c2 loaded together (clamped into N), then
+    // acc <- rstd acc - rstd mean c1 + c2 and the ordinary epilogue
+    f32x4 c1v[TN], c2v[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = min(col0 + j * 16, ep.N - 4);
+      c1v[j] = *reinterpret_cast<const f32x4*>(ep.ln_c1 + col);
+      c2v[j] = *reinterpret_cast<const f32x4*>(ep.ln_c2 + col);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float a = ln_s1[i], b = ln_s2[i];
+      a += __shfl_xor(a, 16, 64);
+      b += __shfl_xor(b, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      b += __shfl_xor(b, 32, 64);
+      const float mean = a * ep.ln_invk;
+      const float var = fmaxf(b * ep.ln_invk - mean * mean, 0.0f);
+      const float r = rsqrtf(var + ep.ln_eps), rm = r * mean;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = ln_fold4(acc[i][j], c1v[j], c2v[j], r, rm);
+    }
+  }
   // the batched forms hold every loaded operand in registers: wave tiles of
   // up to 20 blocks (the largest wave tile, 128x64, keeps the per-block form)
   if constexpr (TM * TN <= 20) {
@@ -1443,16 +1512,29 @@ struct NoSplitScope {
   ~NoSplitScope() { t_no_split = prev; }
 };
 
-// "dma_gemm_kernel<BM, BN, WM, WN, NS, PF, RowDesc|ConvDesc>", as the
-// profiler prints the instantiation
-template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS, class Desc>
+// "dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, LNS, RowDesc|ConvDesc>", as
+// the profiler prints the instantiation
+template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS, bool LNS, class Desc>
 static const char* dma_kernel_name() {
   static const std::string n = "dma_gemm_kernel<" + std::to_string(BM) + ", " + std::to_string(BN) +
                                ", " + std::to_string(WM) + ", " + std::to_string(WN) + ", " +
                                std::to_string(NS) + ", " + (PF ? "true" : "false") + ", " +
-                               std::to_string(SPS) + ", " +
+                               std::to_string(SPS) + ", " + (LNS ? "true" : "false") + ", " +
                                (std::is_same<Desc, RowDesc>::value ? "RowDesc" : "ConvDesc") + ">";
   return n.c_str();
+}
+
+// Tile configurations with a LayerNorm-folding instantiation: the ones the
+// LayerNorm-consuming linears of the UNet take (2048- and 8192-row QKV, cross
+// Q and GEGLU shapes), plus their non-prefetch variants.
+template <int BM, int BN, int WM, int WN, int NS, bool PF, int SPS>
+constexpr bool ln_tile() {
+  return (BM == 128 && BN == 80 && WM == 16 && WN == 80 && NS == 3 && !PF && SPS == 2) ||
+         (BM == 128 && BN == 128 && WM == 64 && WN == 32 && NS == 2 && SPS == 1) ||
+         (BM == 128 && BN == 128 && WM == 32 && WN == 64 && NS == 2 && SPS == 1) ||
+         (BM == 256 && BN == 160 && WM == 64 && WN == 80 && NS == 3 && SPS == 1) ||
+         (BM == 256 && BN == 160 && WM == 32 && WN == 160 && NS == 3 && SPS == 1) ||
+         (BM == 128 && BN == 160 && WM == 32 && WN == 80 && SPS == 1);
 }
 template <int BM, int BN, int WM, int WN, bool DEEP, class Desc>
 static const char* mfma_kernel_name() {
@@ -1482,11 +1564,23 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
       sp = SplitArgs{S, kps, w->ws, w->cnt};
   }
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
-  const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
-  note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, Desc>());
   note_dims(M, N, bd.K, (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0));
-  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, Desc>), dim3(grid), dim3(NT), 0, s, ad,
-                     bd, ep, tiles_m, tiles_n, sp);
+  if (ep.ln_c1) {
+    if constexpr (std::is_same<Desc, RowDesc>::value && ln_tile<BM, BN, WM, WN, NS, PF, SPS>()) {
+      sp = SplitArgs{1, nk, nullptr, nullptr};
+      note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, true, Desc>());
+      hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, true, Desc>), dim3(tiles), dim3(NT),
+                         0, s, ad, bd, ep, tiles_m, tiles_n, sp);
+      DLM_LAUNCH_CHECK();
+      return DLM_OK;
+    } else {
+      return fail(DLM_ERR_UNSUPPORTED, "LayerNorm-folding GEMM: tile without a folding kernel");
+    }
+  }
+  const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
+  note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, false, Desc>());
+  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, false, Desc>), dim3(grid), dim3(NT), 0,
+                     s, ad, bd, ep, tiles_m, tiles_n, sp);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
@@ -1565,6 +1659,43 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
   if ((ep.y_f32 || ep.res_f32) && (ep.vt || ep.act == DLM_ACT_GEGLU))
     return fail(DLM_ERR_UNSUPPORTED, "fp32 output/residual with a GEGLU or V^T epilogue");
   const bool dma = dma_epilogue_ok(ep) && dma_operand_ok(ad) && dma_operand_ok(bd);
+  if (ep.ln_c1) {
+    // LayerNorm-folding linears: the tiles of the plain heuristic below for the
+    // UNet's shapes, 128x128 prefetch tiles for any other
+    if constexpr (!std::is_same<Desc, RowDesc>::value) {
+      return fail(DLM_ERR_UNSUPPORTED, "LayerNorm folding applies to linears only");
+    } else {
+      if (!dma) return fail(DLM_ERR_UNSUPPORTED, "LayerNorm-folding GEMM needs aligned operands");
+      switch (g_forced_tile) {  // tuning aid: the tiles with a folding kernel
+        case 24: return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
+        case 28: return launch_dma<256, 160, 64, 80, 3, true>(ad, bd, ep, M, N, s);
+        case 29: return launch_dma<128, 128, 64, 32, 2, true>(ad, bd, ep, M, N, s);
+        case 31: return launch_dma<128, 160, 32, 80, 3, true>(ad, bd, ep, M, N, s);
+        case 35: return launch_dma<128, 80, 16, 80, 3, false, 2>(ad, bd, ep, M, N, s);
+        case 40: return launch_dma<128, 128, 32, 64, 2, true>(ad, bd, ep, M, N, s);
+        case 41: return launch_dma<256, 160, 32, 160, 3, true>(ad, bd, ep, M, N, s);
+        case 0: break;
+        default: return fail(DLM_ERR_UNSUPPORTED, "forced tile has no LayerNorm-folding kernel");
+      }
+      // Every wave accumulates the statistics of its own rows, so waves that
+      // hold fewer row blocks (and fewer waves sharing rows) spend less VALU
+      // on them.  Measured against LayerNorm + linear, graph-replayed (us):
+      // QKV 2048x3840x1280 128x128 (32x64 waves) 35.4 vs 43.5; cross Q
+      // 2048x1280x1280 128x80 15.7 vs 23.5; GEGLU 2048x10240x1280 256x160
+      // (32x160 waves) 79.9 vs 86.7; 8192 rows: QKV 41.3 vs 45.7, Q 18.0 vs
+      // 26.4, GEGLU 99.4 vs 100.3.
+      const long long t256 = ceil_div(M, 256) * (N / 160), t80 = ceil_div(M, 128) * (N / 80);
+      const long long t160 = ceil_div(M, 128) * (N / 160);
+      const int nk = (int)ceil_div(bd.K, BK);
+      if (ep.act == DLM_ACT_GEGLU && N % 160 == 0 && t256 >= kCUs)
+        return launch_dma<256, 160, 32, 160, 3, true>(ad, bd, ep, M, N, s);
+      if (!ep.vt && ep.act != DLM_ACT_GEGLU && N % 80 == 0 && t80 >= kCUs * 3 / 4 && t80 <= kCUs)
+        return launch_dma<128, 80, 16, 80, 3, false, 2>(ad, bd, ep, M, N, s);
+      if (!ep.vt && ep.act != DLM_ACT_GEGLU && N % 160 == 0 && N <= 1280 && t160 >= kCUs && nk <= 100)
+        return launch_dma<128, 160, 32, 80, 4>(ad, bd, ep, M, N, s);
+      return launch_dma<128, 128, 32, 64, 2, true>(ad, bd, ep, M, N, s);
+    }
+  }
   if (dma) {
     switch (g_forced_tile) {
       case 8: return launch_dma<128, 128, 64, 64, 2>(ad, bd, ep, M, N, s);
@@ -1599,6 +1730,8 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       case 37: return launch_dma<128, 160, 32, 80, 2, false, 2>(ad, bd, ep, M, N, s);
       case 38: return launch_dma<128, 128, 64, 32, 2, false, 2>(ad, bd, ep, M, N, s);
       case 39: return launch_dma<128, 64, 64, 32, 3, false, 2>(ad, bd, ep, M, N, s);
+      case 40: return launch_dma<128, 128, 32, 64, 2, true>(ad, bd, ep, M, N, s);
+      case 41: return launch_dma<256, 160, 32, 160, 3, true>(ad, bd, ep, M, N, s);
       default: break;
     }
     if (g_forced_tile == 0) {
@@ -1882,6 +2015,50 @@ int conv_weight_pack(const void* w, void* out, int Cout, int Cin, int KH, int KW
   return DLM_OK;
 }
 
+// LayerNorm folded into a following linear, weight side: row n of W_out is
+// fp16(W[n] * gamma) (gamma absent: a copy), c1[n] = sum_k W_out[n][k] (of the
+// rounded values), c2[n] = sum_k beta[k] W[n][k] + bias[n], both in fp32.
+// One 256-thread block per row; fixed-order reduction (deterministic).
+__global__ void ln_fold_kernel(const f16* __restrict__ w, int ldw, int K,
+                               const f16* __restrict__ gamma, const f16* __restrict__ beta,
+                               const f16* __restrict__ bias, f16* __restrict__ wo, int ldo,
+                               float* __restrict__ c1, float* __restrict__ c2) {
+  const int n = blockIdx.x, tid = threadIdx.x;
+  const f16* wr = w + (size_t)n * ldw;
+  f16* orow = wo + (size_t)n * ldo;
+  float a = 0.0f, b = 0.0f;
+  for (int k = tid; k < K; k += blockDim.x) {
+    const float x = (float)wr[k];
+    const f16 f = (f16)(gamma ? x * (float)gamma[k] : x);
+    orow[k] = f;
+    a += (float)f;
+    if (beta) b = __builtin_fmaf((float)beta[k], x, b);
+  }
+  __shared__ float ra[256], rb[256];
+  ra[tid] = a;
+  rb[tid] = b;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) {
+      ra[tid] += ra[tid + o];
+      rb[tid] += rb[tid + o];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    c1[n] = ra[0];
+    c2[n] = rb[0] + (bias ? (float)bias[n] : 0.0f);
+  }
+}
+
+int ln_fold(const void* w, int ldw, int N, int K, const void* gamma, const void* beta,
+            const void* bias, void* wo, int ldo, float* c1, float* c2, hipStream_t s) {
+  DLM_LAUNCH("ln_fold_kernel", ln_fold_kernel, dim3(N), dim3(256), 0, s, (const f16*)w, ldw, K,
+             (const f16*)gamma, (const f16*)beta, (const f16*)bias, (f16*)wo, ldo, c1, c2);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Convolution (channels-last) host entry.
 // ---------------------------------------------------------------------------
@@ -2027,6 +2204,75 @@ int dlm_linear_f32out_fp16(const void* X, int lda, const void* W, int ldw, const
   ep.y_f32 = 1;
   ep.res_f32 = 1;
   return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
+}
+
+int dlm_linear_ln_fp16(const void* X, int lda, const void* W, int ldw, const float* c1,
+                       const float* c2, float eps, const void* R, int ldr, void* Y, int ldy, int M,
+                       int N, int K, float beta, int act, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(X && W && Y && c1 && c2, "NULL operand");
+  DLM_REQUIRE(K % 64 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K must be a multiple of 64, lda and ldw of 8");
+  DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
+  DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W) && dlm_aligned16(c1) && dlm_aligned16(c2),
+              "X, W, c1 and c2 must be 16-byte aligned");
+  DLM_REQUIRE(2LL * M * lda < (1LL << 31) && 2LL * N * ldw < (1LL << 31), "X or W larger than 2 GiB");
+  DLM_REQUIRE(act == DLM_ACT_NONE || act == DLM_ACT_SILU || act == DLM_ACT_GELU || act == DLM_ACT_GEGLU,
+              "unknown act");
+  DLM_REQUIRE(eps >= 0.0f, "eps must be non-negative");
+  if (act == DLM_ACT_GEGLU) {
+    DLM_REQUIRE(N % 16 == 0, "GEGLU needs N (interleaved value+gate columns) % 16 == 0");
+    DLM_REQUIRE(ldy >= N / 2 && (!R || ldr >= N / 2), "ldy/ldr smaller than N/2");
+  } else {
+    DLM_REQUIRE(N % 4 == 0, "N must be a multiple of 4");
+    DLM_REQUIRE(ldy >= N && (!R || ldr >= N), "ldy/ldr smaller than N");
+  }
+  RowDesc ad{(const f16*)X, lda, M, K, (unsigned)((size_t)M * lda * 2)};
+  RowDesc bd{(const f16*)W, ldw, N, K, (unsigned)((size_t)N * ldw * 2)};
+  EpiArgs ep = make_epi(Y, ldy, nullptr, R, ldr, M, N, 1.0f, beta, act);
+  ep.ln_c1 = c1;
+  ep.ln_c2 = c2;
+  ep.ln_invk = 1.0f / (float)K;
+  ep.ln_eps = eps;
+  return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
+}
+
+int dlm_linear_vt_ln_fp16(const void* X, int lda, const void* W, int ldw, const float* c1,
+                          const float* c2, float eps, void* Y, int ldy, void* VT, int vt_col0,
+                          int tokens, int vt_ld, int M, int N, int K, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(X && W && Y && VT && c1 && c2, "NULL operand");
+  DLM_REQUIRE(K % 64 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K must be a multiple of 64, lda and ldw of 8");
+  DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
+  DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W) && dlm_aligned16(c1) && dlm_aligned16(c2),
+              "X, W, c1 and c2 must be 16-byte aligned");
+  DLM_REQUIRE(2LL * M * lda < (1LL << 31) && 2LL * N * ldw < (1LL << 31), "X or W larger than 2 GiB");
+  DLM_REQUIRE(vt_col0 >= 0 && vt_col0 < N && vt_col0 % 4 == 0 && N % 4 == 0,
+              "vt_col0 must be a multiple of 4 inside [0, N), N % 4 == 0");
+  DLM_REQUIRE(tokens > 0 && M % tokens == 0, "M must be a whole number of samples of `tokens` rows");
+  DLM_REQUIRE(vt_ld >= tokens, "vt_ld smaller than tokens");
+  DLM_REQUIRE(ldy >= vt_col0 && ldy % 4 == 0, "ldy must cover the columns before vt_col0");
+  DLM_REQUIRE(((uintptr_t)Y & 7) == 0, "Y must be 8-byte aligned");
+  DLM_REQUIRE(eps >= 0.0f, "eps must be non-negative");
+  RowDesc ad{(const f16*)X, lda, M, K, (unsigned)((size_t)M * lda * 2)};
+  RowDesc bd{(const f16*)W, ldw, N, K, (unsigned)((size_t)N * ldw * 2)};
+  EpiArgs ep = make_epi(Y, ldy, nullptr, nullptr, 0, M, N, 1.0f, 0.0f, DLM_ACT_NONE);
+  ep.vt = (f16*)VT;
+  ep.vt_col0 = vt_col0;
+  ep.vt_tokens = tokens;
+  ep.vt_ld = vt_ld;
+  ep.ln_c1 = c1;
+  ep.ln_c2 = c2;
+  ep.ln_invk = 1.0f / (float)K;
+  ep.ln_eps = eps;
+  return launch_gemm(ad, bd, ep, M, N, (hipStream_t)stream);
+}
+
+int dlm_ln_fold_fp16(const void* W, int ldw, int N, int K, const void* gamma, const void* beta,
+                     const void* bias, void* W_out, int ldo, float* c1, float* c2, void* stream) {
+  if (N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(W && W_out && c1 && c2, "NULL operand");
+  DLM_REQUIRE(ldw >= K && ldo >= K, "ldw/ldo smaller than K");
+  return ln_fold(W, ldw, N, K, gamma, beta, bias, W_out, ldo, c1, c2, (hipStream_t)stream);
 }
 
 int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, float alpha,
@@ -2326,7 +2572,7 @@ extern "C" int dlm_gemm_force_split(int splits) {
 }
 
 extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 39 && splits >= 0 && splits <= 64, "bad tile / split");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 41 && splits >= 0 && splits <= 64, "bad tile / split");
   if (M == 0 && N == 0 && K == 0) {
     dlm::g_overrides.clear();
     return DLM_OK;
@@ -2342,7 +2588,7 @@ extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int spl
 }
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 39, "tile_id must be in [0, 39]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 41, "tile_id must be in [0, 41]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

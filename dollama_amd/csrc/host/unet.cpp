@@ -210,12 +210,20 @@ void UNet::apply_lora(const std::string& key, const void* dA, const void* dB, in
     DLM_CALL(dlm_conv_weight_pack_add_fp16(delta, pl.dst, pl.Co, pl.Ci, pl.k, pl.k, pl.cin_pad,
                                            pl.ld, pl.col0, stream));
   }
+  auto fd = fold_deps_.find(key);
+  if (fd != fold_deps_.end())
+    for (const LnFold& f : fd->second) refold(f, stream);
   DLM_CALL(dlm_stream_synchronize(stream));  // the arena scope ends here
 }
 
 void UNet::clear_loras(void* stream) {
   for (auto it = backups_.rbegin(); it != backups_.rend(); ++it)
     DLM_CALL(dlm_memcpy_async(it->dst, it->copy, it->bytes, 2, stream));
+  for (const std::string& key : patched_) {  // folds of restored weights
+    auto fd = fold_deps_.find(key);
+    if (fd != fold_deps_.end())
+      for (const LnFold& f : fd->second) refold(f, stream);
+  }
   DLM_CALL(dlm_stream_synchronize(stream));
   for (Backup& b : backups_) dlm_free(b.copy);
   backups_.clear();
@@ -351,6 +359,35 @@ const void* UNet::copy_of(const std::string& name, const Shape& shape, void* str
   return dst;
 }
 
+UNet::LnFold UNet::make_fold(const void* w, const void* g, const void* b, const void* bias, int N,
+                             int K, const std::vector<std::string>& deps, void* stream) {
+  LnFold f;
+  f.w = w;
+  f.g = g;
+  f.b = b;
+  f.bias = bias;
+  f.N = N;
+  f.K = K;
+  f.wf = take((size_t)N * K);
+  f.c1 = static_cast<float*>(take((size_t)2 * N));  // fp32: two halves per element
+  f.c2 = static_cast<float*>(take((size_t)2 * N));
+  if (!sizing_) {
+    refold(f, stream);
+    for (const std::string& d : deps) fold_deps_[d].push_back(f);
+  }
+  return f;
+}
+
+void UNet::refold(const LnFold& f, void* stream) {
+  DLM_CALL(dlm_ln_fold_fp16(f.w, f.K, f.N, f.K, f.g, f.b, f.bias, f.wf, f.K, f.c1, f.c2, stream));
+}
+
+void UNet::set_ln_fold(int mask) {
+  if (mask < 0 || mask > 3) throw std::invalid_argument("UNet::set_ln_fold: mask must be in [0, 3]");
+  if (mask != ln_fold_) clear_graphs();
+  ln_fold_ = mask;
+}
+
 void UNet::place_copy(const std::string& name, void* dst, size_t n) {
   Placement pl;
   pl.kind = Placement::kCopy;
@@ -483,6 +520,13 @@ UNet::T2D UNet::pack_t2d(const std::string& p, int C, int depth, void* stream) {
     k.bff1 = b1;
     k.wff2 = copy_of(b + "ff.net.2.weight", {C, 4 * C}, stream);
     k.bff2 = copy_of(b + "ff.net.2.bias", {C}, stream);
+    // folded copies of the LayerNorm-consuming linears
+    k.fqkv = make_fold(k.wqkv, k.ln1g, k.ln1b, nullptr, 3 * C, C,
+                       {b + "attn1.to_q.weight", b + "attn1.to_k.weight", b + "attn1.to_v.weight",
+                        b + "norm1.weight", b + "norm1.bias"},
+                       stream);
+    k.fq2 = make_fold(k.wq2, k.ln2g, k.ln2b, nullptr, C, C,
+                      {b + "attn2.to_q.weight", b + "norm2.weight", b + "norm2.bias"}, stream);
     k.kv_off = kv_total_ / 2;  // row offset of this block's K (and, past all K rows, its V)
     kv_total_ += 2 * C;
     t.blocks.push_back(k);
@@ -624,6 +668,7 @@ void UNet::prepare(void* stream) {
   backups_.clear();
   patched_.clear();
   placed_.clear();
+  fold_deps_.clear();
   // pass 1: sizes and validation
   sizing_ = true;
   pack_all(stream);
@@ -778,12 +823,19 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
   const int vt_ld = ts.vt_ld;
   void* o = ts.o;
   void* f = ts.f;
-  // self-attention
-  LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
-  // Q|K as [M, 2C] and V transposed per sample as [B, heads, 64, HW]
-  LAUNCH(kLinear, 2.0 * M * 3 * C * C, lin_bytes(M, 3 * C, C, 3 * C, false),
-         dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, vt_ld, M,
-                            3 * C, C, stream));
+  // self-attention: Q|K as [M, 2C] and V transposed per sample as
+  // [B, heads, 64, HW], of norm1(h) (folded into the GEMM, or a separate
+  // LayerNorm launch)
+  if (ln_fold_ & 1) {
+    LAUNCH(kLinear, 2.0 * M * 3 * C * C, lin_bytes(M, 3 * C, C, 3 * C, false),
+           dlm_linear_vt_ln_fp16(h, C, k.fqkv.wf, C, k.fqkv.c1, k.fqkv.c2, 1e-5f, qkv, 2 * C, vt,
+                                 2 * C, HW, vt_ld, M, 3 * C, C, stream));
+  } else {
+    LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln1g, k.ln1b, n, M, C, 1e-5f, stream));
+    LAUNCH(kLinear, 2.0 * M * 3 * C * C, lin_bytes(M, 3 * C, C, 3 * C, false),
+           dlm_linear_vt_fp16(n, C, k.wqkv, C, nullptr, qkv, 2 * C, vt, 2 * C, HW, vt_ld, M,
+                              3 * C, C, stream));
+  }
   {
     dlm_attention_vt_args a{};
     const char* base = static_cast<const char*>(qkv);
@@ -814,10 +866,16 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
        dlm_linear_fp16(o, C, k.wo1, C, k.bo1, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
                            stream));
   // cross-attention over the context's K / V^T (rows kv_off.. of stride kv_stride)
-  LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln2g, k.ln2b, n, M, C, 1e-5f, stream));
-  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, false),
-       dlm_linear_fp16(n, C, k.wq2, C, nullptr, nullptr, 0, qkv, C, M, C, C, 1.0f, 0.0f,
+  if (ln_fold_ & 2) {
+    LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, false),
+           dlm_linear_ln_fp16(h, C, k.fq2.wf, C, k.fq2.c1, k.fq2.c2, 1e-5f, nullptr, 0, qkv, C, M, C, C,
+                              0.0f, DLM_ACT_NONE, stream));
+  } else {
+    LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln2g, k.ln2b, n, M, C, 1e-5f, stream));
+    LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, false),
+           dlm_linear_fp16(n, C, k.wq2, C, nullptr, nullptr, 0, qkv, C, M, C, C, 1.0f, 0.0f,
                            DLM_ACT_NONE, stream));
+  }
   {
     dlm_attention_vt_args a{};
     a.q = qkv;
@@ -849,11 +907,12 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
   LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
        dlm_linear_fp16(o, C, k.wo2, C, k.bo2, h, C, h, C, M, C, C, 1.0f, 1.0f, DLM_ACT_NONE,
                            stream));
-  // GEGLU feed-forward
+  // GEGLU feed-forward (norm3 stays a separate launch: folded into the
+  // GEGLU projection it made the step slower, 23.07 -> 23.54 ms)
   LAUNCH(kLayerNorm, 0.0, 4.0 * M * C, dlm_layer_norm_fp16(h, k.ln3g, k.ln3b, n, M, C, 1e-5f, stream));
   LAUNCH(kLinear, 2.0 * M * 8 * C * C, lin_bytes(M, 8 * C, C, 4 * C, false),
-       dlm_linear_fp16(n, C, k.wff1, C, k.bff1, nullptr, 0, f, 4 * C, M, 8 * C, C, 1.0f,
-                           0.0f, DLM_ACT_GEGLU, stream));
+         dlm_linear_fp16(n, C, k.wff1, C, k.bff1, nullptr, 0, f, 4 * C, M, 8 * C, C, 1.0f,
+                         0.0f, DLM_ACT_GEGLU, stream));
   LAUNCH(kLinear, 2.0 * M * 4 * C * C, lin_bytes(M, C, 4 * C, C, true),
        dlm_linear_fp16(f, 4 * C, k.wff2, 4 * C, k.bff2, h, C, h, C, M, C, 4 * C, 1.0f, 1.0f,
                            DLM_ACT_NONE, stream));

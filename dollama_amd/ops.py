@@ -332,6 +332,59 @@ def linear_vt(x: torch.Tensor, w: torch.Tensor, vt_col0: int, tokens: int, bias=
     return y, vt
 
 
+def ln_fold(w: torch.Tensor, gamma=None, beta=None, bias=None):
+    """Weight side of a LayerNorm folded into the linear w [N, K] (bias [N]):
+    (fp16 w * gamma, fp32 c1 = row sums of it, fp32 c2 = w @ beta + bias)."""
+    N, K = w.shape
+    wo = torch.empty_like(w)
+    c1 = torch.empty(N, dtype=torch.float32, device=w.device)
+    c2 = torch.empty(N, dtype=torch.float32, device=w.device)
+    _need(w, N * K, "w")
+    _need(gamma, K, "gamma", optional=True)
+    _need(beta, K, "beta", optional=True)
+    _need(bias, N, "bias", optional=True)
+    call("dlm_ln_fold_fp16", _p(w), K, N, K, _p(gamma), _p(beta), _p(bias), _p(wo), K, _p(c1),
+         _p(c2), stream_handle())
+    return wo, c1, c2
+
+
+def linear_ln(x: torch.Tensor, w_folded, c1, c2, eps: float, residual=None, act=ACT_NONE,
+              out=None, beta=1.0) -> torch.Tensor:
+    """y = act(LayerNorm(x) @ w.T + b) + beta * residual with the LayerNorm
+    computed inside the GEMM; w_folded, c1, c2 from ``ln_fold``."""
+    M, K = x.shape
+    N = w_folded.shape[0]
+    ncols = N // 2 if act == ACT_GEGLU else N
+    if out is None:
+        out = torch.empty(M, ncols, dtype=torch.float16, device=x.device)
+    _need(x, M * K, "x")
+    _need(w_folded, N * K, "w")
+    _need(c1, N, "c1", dtype=torch.float32)
+    _need(c2, N, "c2", dtype=torch.float32)
+    _need(residual, M * ncols, "residual", optional=True)
+    _need(out, M * ncols, "out")
+    call("dlm_linear_ln_fp16", _p(x), K, _p(w_folded), K, _p(c1), _p(c2), float(eps), _p(residual),
+         ncols, _p(out), ncols, M, N, K, float(beta), int(act), stream_handle())
+    return out
+
+
+def linear_vt_ln(x: torch.Tensor, w_folded, c1, c2, eps: float, vt_col0: int, tokens: int,
+                 vt_ld=None):
+    """``linear_vt`` of LayerNorm(x), the LayerNorm computed inside the GEMM."""
+    vt_ld = vt_ld or tokens
+    M, K = x.shape
+    N = w_folded.shape[0]
+    y = torch.empty(M, vt_col0, dtype=torch.float16, device=x.device)
+    vt = torch.empty(M // tokens, N - vt_col0, vt_ld, dtype=torch.float16, device=x.device)
+    _need(x, M * K, "x")
+    _need(w_folded, N * K, "w")
+    _need(c1, N, "c1", dtype=torch.float32)
+    _need(c2, N, "c2", dtype=torch.float32)
+    call("dlm_linear_vt_ln_fp16", _p(x), K, _p(w_folded), K, _p(c1), _p(c2), float(eps), _p(y),
+         vt_col0, _p(vt), vt_col0, tokens, vt_ld, M, N, K, stream_handle())
+    return y, vt
+
+
 def pack_geglu(w: torch.Tensor, b: Optional[torch.Tensor]):
     """[2d, K] value-first GEGLU projection -> 4-row value/gate interleave for ACT_GEGLU."""
     two_d, K = w.shape

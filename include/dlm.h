@@ -257,6 +257,30 @@ int dlm_linear_f32out_fp16(const void* X, int lda, const void* W, int ldw, const
                            const float* R, int ldr, float* Y, int ldy, int M, int N, int K,
                            float alpha, float beta, int act, void* stream);
 
+/* LayerNorm folded into the linear that consumes it (no LayerNorm launch,
+ * no normalised copy of X):
+ *   Y = act(LN(X) W0^T + b) + beta * R,  LN(X) = (X - mean) * rstd * gamma + lnbeta
+ * with per-row mean and variance over X's K columns (one pass in fp32:
+ * var = max(E[x^2] - mean^2, 0), rstd = 1 / sqrt(var + eps), as
+ * launch_layer_norm computes them, src/kernels/layernorm.cu:78-126),
+ * computed inside the GEMM from the X operand it multiplies.  W, c1, c2 come
+ * from dlm_ln_fold_fp16(W0, gamma, lnbeta, b); W may be GEGLU-packed (fold
+ * after dlm_geglu_pack_fp16, with the packed bias).  K % 64 == 0; c1, c2
+ * 16-byte aligned.  Same epilogue options as dlm_linear_fp16 / _vt_fp16
+ * (no bias argument: it is inside c2).  No counterpart entry in the
+ * reference, whose LayerNorm is a separate launch. */
+int dlm_linear_ln_fp16(const void* X, int lda, const void* W, int ldw, const float* c1,
+                       const float* c2, float eps, const void* R, int ldr, void* Y, int ldy, int M,
+                       int N, int K, float beta, int act, void* stream);
+int dlm_linear_vt_ln_fp16(const void* X, int lda, const void* W, int ldw, const float* c1,
+                          const float* c2, float eps, void* Y, int ldy, void* VT, int vt_col0,
+                          int tokens, int vt_ld, int M, int N, int K, void* stream);
+/* Weight side of the fold: W_out[n] = fp16(W[n] * gamma) (a copy when gamma
+ * is NULL), c1[n] = sum_k W_out[n][k], c2[n] = sum_k lnbeta[k] W[n][k] + b[n]
+ * (fp32; lnbeta / b may be NULL).  W_out may alias W. */
+int dlm_ln_fold_fp16(const void* W, int ldw, int N, int K, const void* gamma, const void* lnbeta,
+                     const void* b, void* W_out, int ldo, float* c1, float* c2, void* stream);
+
 /* Repack GEGLU projection weight [2d, K] and bias [2d] (value rows first, as
  * diffusers stores them) into the 4-row value/gate interleave DLM_ACT_GEGLU
  * expects: packed row 8q+s holds value row 4q+s (s < 4) or gate row

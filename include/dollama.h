@@ -136,6 +136,15 @@ int dlm_unet_set_stage_hook(void* handle, dlm_unet_stage_hook hook, void* user);
 int dlm_unet_set_graphs(void* handle, int on);
 int dlm_unet_graphs_captured(void* handle, size_t* count);
 
+/* Which of the transformer blocks' LayerNorms are folded into the linears
+ * that consume them (see dlm_linear_ln_fp16), as a bit mask in [0, 3]: bit 0
+ * norm1 -> fused QKV, bit 1 norm2 -> cross-attention Q (3, both, is the
+ * default); an unfolded LayerNorm, and norm3 always, runs as its own launch.
+ * No counterpart in the reference (its forward is the unfolded one; the
+ * folded form computes the same function).  The folded weight copies are
+ * kept in step with LoRA patches and their removal. */
+int dlm_unet_set_ln_fold(void* handle, int mask);
+
 /* Per-launch kernel timing (device events around every launch of a
  * forward).  Classes: 0 conv, 1 linear, 2 attention, 3 groupnorm,
  * 4 layernorm, 5 other.  report fills, per class, out[4*c + 0..3] =

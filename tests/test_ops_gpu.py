@@ -55,9 +55,9 @@ def test_linear_geglu(gpu, M, d, K):
     assert_close(y, R.geglu(R.linear(x, w, b)), f"geglu {M}x{d}x{K}")
 
 
-@pytest.mark.parametrize("tile", list(range(8, 40)))
+@pytest.mark.parametrize("tile", list(range(8, 42)))
 def test_dma_tile_configs(gpu, tile):
-    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-39, the
+    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-41, the
     fragment-prefetch forms 27-34 and two-slice stages 35-39 included),
     whole and split-K, on ragged shapes with an odd slice count and a K tail:
     bias + SiLU + residual, GEGLU, and a 3x3 conv with residual."""
@@ -386,6 +386,51 @@ def test_attention_vt(gpu, B, H, Sq, Sk):
                      o_strides=(Sq * C, C, Dh), scale=0.125)
     ref = torch.cat([R.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], 0.125) for b in range(B)])
     assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), "attention_vt")
+
+
+@pytest.mark.parametrize("M,N,K,act,vt", [
+    (2048, 1280, 1280, 0, False), (8192, 640, 640, 0, False), (2048, 3840, 1280, 0, True),
+    (8192, 1920, 640, 0, True), (2048, 10240, 1280, 4, False), (8192, 5120, 640, 4, False),
+    (300, 96, 192, 0, False), (130, 160, 128, 4, False)])
+def test_linear_layernorm_folded(gpu, M, N, K, act, vt):
+    """LayerNorm folded into the consuming linear (the UNet's QKV, cross-Q and
+    GEGLU shapes, plus ragged ones): gamma in the weight columns, per-row
+    statistics accumulated inside the GEMM, against LayerNorm then linear in
+    fp32 on the CPU.  Rows carry an offset (mean 0.5, std 2)."""
+    act = ops.ACT_GEGLU if act == 4 else ops.ACT_NONE
+    announce(f"linear_ln M={M} N={N} K={K} act={act} vt={vt}")
+    x = randn((M, K), 140, std=2.0, mean=0.5)
+    g, b = randn((K,), 141, std=0.3, mean=1.0), randn((K,), 142, std=0.3)
+    w, bias = randn((N, K), 143, std=0.04), randn((N,), 144, std=0.1)
+    ref = R.linear(R.layer_norm(x, g, b, 1e-5), w, bias)
+    wg, bg = to_gpu(w), to_gpu(bias)
+    if act == ops.ACT_GEGLU:
+        wg, bg = ops.pack_geglu(wg, bg)
+        ref = R.geglu(ref)
+    wf, c1, c2 = ops.ln_fold(wg, to_gpu(g), to_gpu(b), bg)
+    if vt:
+        C = N // 3
+        y, vtt = ops.linear_vt_ln(to_gpu(x), wf, c1, c2, 1e-5, 2 * C, 1024)
+        assert_close(y, ref[:, :2 * C], "linear_vt_ln y")
+        assert_close(vtt, ref[:, 2 * C:].reshape(M // 1024, 1024, C).transpose(1, 2), "linear_vt_ln vt")
+    else:
+        y = ops.linear_ln(to_gpu(x), wf, c1, c2, 1e-5, act=act)
+        assert_close(y, ref, "linear_ln")
+
+
+def test_linear_layernorm_folded_large_offset(gpu):
+    """Rows with mean 40 and std 0.5: the one-pass fp32 statistics (as the
+    reference's LayerNorm) stay accurate; residual and beta in the epilogue."""
+    M, N, K = 1024, 640, 640
+    announce("linear_ln mean 40 / std 0.5, residual")
+    x = randn((M, K), 145, std=0.5, mean=40.0)
+    g, b = randn((K,), 146, std=0.3, mean=1.0), randn((K,), 147, std=0.3)
+    w, bias = randn((N, K), 148, std=0.04), randn((N,), 149, std=0.1)
+    r = randn((M, N), 150)
+    ref = R.linear(R.layer_norm(x.double(), g.double(), b.double(), 1e-5), w.double(), bias.double()).float() + 0.5 * r
+    wf, c1, c2 = ops.ln_fold(to_gpu(w), to_gpu(g), to_gpu(b), to_gpu(bias))
+    y = ops.linear_ln(to_gpu(x), wf, c1, c2, 1e-5, residual=to_gpu(r), beta=0.5)
+    assert_close(y, ref, "linear_ln large offset")
 
 
 @pytest.mark.parametrize("B,S,C,ld", [(2, 1024, 1280, 1024), (2, 64, 128, 64), (3, 40, 192, 40),

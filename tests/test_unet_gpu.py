@@ -83,6 +83,36 @@ def test_unet_tiny_parity_stages(gpu):
     net.close()
 
 
+def test_unet_layernorm_fold_matches_unfolded(gpu):
+    """The LayerNorms folded into their consumers (the default mask 3: norm1 ->
+    QKV, norm2 -> cross-attention Q; each bit alone too) compute the unfolded
+    forward's function: the same noise_pred up to the changed fp32 summation
+    (x sums in the GEMM, gamma folded into the fp16 weight), and every mask
+    repeats bit for bit.  Masks outside [0, 3] are refused."""
+    cfg = TINY
+    print("[case] tiny UNet LayerNorm fold masks 0-3", flush=True)
+    Wc = OR.random_weights(OR.TINY, seed=21)
+    lat, ts, ehs, text, ids = _inputs(cfg, 2, 32, 32, 77, seed=22)
+    net = U.UNet(cfg)
+    net.set_weights(_to_gpu(Wc))
+    net.prepare()
+    args = (lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
+    outs = {}
+    for mask in (0, 1, 2, 3):
+        net.set_ln_fold(mask)
+        a = net.forward(*args).float()
+        b = net.forward(*args).float()
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"mask {mask}: repeat forward not bit-identical"
+        outs[mask] = a.cpu()
+    for mask in (1, 2, 3):
+        assert_close(outs[mask], outs[0], f"fold mask {mask} vs unfolded", rel_tol=5e-3, cos_tol=0.99999)
+    for bad in (-1, 4):
+        with pytest.raises(Exception):
+            net.set_ln_fold(bad)
+    net.close()
+
+
 def test_unet_batch2_equals_two_batch1(gpu):
     cfg = TINY
     H = W = 32
