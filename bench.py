@@ -175,7 +175,8 @@ def replay_kernel(name, problems, dev, seed):
     over the problems it ran in the step: each problem's launches are captured
     into a HIP graph and replayed between one event pair (time_graph), and the
     per-problem times are weighted by the problem's launches per step.  The
-    kernel each launch ran is checked against `name`.  None for convs."""
+    kernel each launch ran is checked against `name`.  None for convs and
+    LayerNorm-folded linears."""
     import ctypes
     import torch
     from dollama_amd import _lib, ops
@@ -190,7 +191,7 @@ def replay_kernel(name, problems, dev, seed):
     tot_us = tot_flop = 0.0
     tot_n = 0
     for (M, N, K, flags), cnt in problems.items():
-        if flags & 256:
+        if flags & (256 | 512):  # convs, LayerNorm-folded linears
             return None
         act, res = (flags >> 4) & 15, flags & 1
         ncols = N // 2 if act == ops.ACT_GEGLU else N

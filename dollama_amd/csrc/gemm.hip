@@ -1564,11 +1564,14 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
       sp = SplitArgs{S, kps, w->ws, w->cnt};
   }
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
-  note_dims(M, N, bd.K, (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0));
+  // the problem's dims (after note_kernel, which clears them)
+  const int dims_flags = (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0) |
+                         (ep.ln_c1 ? 512 : 0);
   if (ep.ln_c1) {
     if constexpr (std::is_same<Desc, RowDesc>::value && ln_tile<BM, BN, WM, WN, NS, PF, SPS>()) {
       sp = SplitArgs{1, nk, nullptr, nullptr};
       note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, true, Desc>());
+      note_dims(M, N, bd.K, dims_flags);
       hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, true, Desc>), dim3(tiles), dim3(NT),
                          0, s, ad, bd, ep, tiles_m, tiles_n, sp);
       DLM_LAUNCH_CHECK();
@@ -1579,6 +1582,7 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   }
   const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
   note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, false, Desc>());
+  note_dims(M, N, bd.K, dims_flags);
   hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, false, Desc>), dim3(grid), dim3(NT), 0,
                      s, ad, bd, ep, tiles_m, tiles_n, sp);
   DLM_LAUNCH_CHECK();

@@ -56,7 +56,8 @@ void dlm_set_last_error(const char* msg);
 const char* dlm_last_kernel(int reset);
 /* Problem of that launch when it was a GEMM or implicit-GEMM conv: dims[0..3]
  * = rows M, output columns N, reduction length K, flags (bit 0: residual
- * epilogue; bits 4-7: activation code; bit 8: conv); zeros otherwise. */
+ * epilogue; bits 4-7: activation code; bit 8: conv; bit 9: LayerNorm folded
+ * in, dlm_linear_ln_fp16); zeros otherwise. */
 int dlm_last_kernel_dims(int* dims);
 int dlm_get_device_count(int* count);
 int dlm_set_device(int device);
