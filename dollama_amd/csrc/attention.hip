@@ -273,6 +273,20 @@ constexpr int FA_STAGE = 2 * FA_TILE;
 constexpr int FA_NS = 3;
 constexpr int kFaOOB = (int)0x80000000;
 
+// x of this lane and of lane ^ 32, as the pair (s[0], s[1]) in some order:
+// v_permlane32_swap exchanges the upper half of its first operand with the
+// lower half of its second, so with x in both every lane ends holding its
+// own value and its partner's (a VALU op; a shuffle is an LDS round trip).
+// max and + over the pair are symmetric, so the results equal the shuffle's.
+__device__ __forceinline__ float fa_max_halves(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float fa_sum_halves(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
 // Software pipeline, one 32-query block per wave (more waves beat sharing
 // K/V fragments between two blocks: the softmax is VALU work that other
 // waves' MFMAs hide): the scores of tile kt+1 (MFMA) are issued before the
@@ -321,28 +335,33 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
 
   const i32x4 rk = fa_rsrc(p.k, p.k_bytes);
   const i32x4 rv = fa_rsrc(p.vt, p.vt_bytes);
-  int koff[DI], kkey[DI], voff[DI], vkey[DI];
+  // DMA instruction i of this wave: LDS row r of the tile, 16-byte chunk c of
+  // it; the K row holds key fa_perm(r), the V^T row's chunk keys 8c .. 8c+7
+  auto dma_row = [&](int i) { return (wave * DI + i) * 8 + (lane >> 3); };
+  auto dma_chunk = [&](int r) { return (lane & 7) ^ ((r >> 1) & 7); };
+  int koff[DI], voff[DI];
 #pragma unroll
   for (int i = 0; i < DI; ++i) {
-    const int r = (wave * DI + i) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    kkey[i] = fa_perm(r);
-    koff[i] = (int)((b * p.k_sb + h * p.k_sh + (long long)kkey[i] * p.k_ss + c * 8) * 2);
-    vkey[i] = c * 8;
+    const int r = dma_row(i), c = dma_chunk(r);
+    koff[i] = (int)((b * p.k_sb + h * p.k_sh + (long long)fa_perm(r) * p.k_ss + c * 8) * 2);
     voff[i] = (int)((b * p.vt_sb + h * p.vt_sh + (long long)r * p.vt_ld + c * 8) * 2);
   }
   const int kstep = (int)(FA_TK * p.k_ss * 2);
+  // keys past Sk exist only in a partial last tile; their rows and chunks are
+  // recomputed there rather than held in registers for the whole loop
   auto issue = [&](int buf, int kt) {
     unsigned char DLM_LDS* st = smem + buf * FA_STAGE;
+    const int k0 = kt * FA_TK;
+    const bool part = k0 + FA_TK > p.Sk;
 #pragma unroll
     for (int i = 0; i < DI; ++i) {
-      const int key = kt * FA_TK + kkey[i];
-      fa_dma16(rk, st + (wave * DI + i) * 1024, key < p.Sk ? koff[i] + kt * kstep : kFaOOB);
+      const bool in = !part || k0 + fa_perm(dma_row(i)) < p.Sk;
+      fa_dma16(rk, st + (wave * DI + i) * 1024, in ? koff[i] + kt * kstep : kFaOOB);
     }
 #pragma unroll
     for (int i = 0; i < DI; ++i) {
-      const int key = kt * FA_TK + vkey[i];
-      fa_dma16(rv, st + FA_TILE + (wave * DI + i) * 1024, key < p.Sk ? voff[i] + kt * (FA_TK * 2) : kFaOOB);
+      const bool in = !part || k0 + dma_chunk(dma_row(i)) * 8 < p.Sk;
+      fa_dma16(rv, st + FA_TILE + (wave * DI + i) * 1024, in ? voff[i] + kt * (FA_TK * 2) : kFaOOB);
     }
   };
   auto frag = [&](const unsigned char DLM_LDS* st, int row, int chunk) -> f16x8 {
@@ -382,7 +401,7 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sv[kb][e]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = fa_max_halves(mt);
     const bool grow = (mt - m_run) * p.c > 8.0f;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       asm volatile("" ::: "memory");  // a real branch: never evaluated speculatively
@@ -434,11 +453,10 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  f32x16 sc[2];
-  scores(smem, sc);
 
+  // one tile: sc holds its scores, the next tile's scores go to sn
   int cur = 0;
-  for (int kt = 0; kt + 1 < nkt; ++kt) {
+  auto step = [&](int kt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
     const int nxt = cur == FA_NS - 1 ? 0 : cur + 1;
     const int nn = nxt == FA_NS - 1 ? 0 : nxt + 1;
     FA_WAIT_VM(0);  // tile kt+1 (this wave's part)
@@ -447,19 +465,16 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 2 < nkt) issue(nn, kt + 2);
     const unsigned char DLM_LDS* st = smem + cur * FA_STAGE;
-    f32x16 sn[2];
     scores(smem + nxt * FA_STAGE, sn);  // tile kt+1, in the shadow of the softmax below
     f16x8 vf[8];
     vread(st, vf);
     f16x8 pf[4];
     softmax(sc, pf);  // tiles before the last are full: no mask
     pv(vf, pf);
-    sc[0] = sn[0];
-    sc[1] = sn[1];
     cur = nxt;
-  }
+  };
   // last tile: its keys may end inside the tile
-  {
+  auto last = [&](f32x16 (&sc)[2]) {
     const int kt = nkt - 1;
     if (kt * FA_TK + FA_TK > p.Sk) {
 #pragma unroll
@@ -475,6 +490,21 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     f16x8 pf[4];
     softmax(sc, pf);
     pv(vf, pf);
+  };
+  // two tiles per iteration with the score buffers swapping roles, so no
+  // loop-carried copy of the next tile's 32 scores is needed
+  f32x16 sa[2], sb[2];
+  scores(smem, sa);
+  int kt = 0;
+  for (; kt + 2 < nkt; kt += 2) {
+    step(kt, sa, sb);
+    step(kt + 1, sb, sa);
+  }
+  if (kt + 1 < nkt) {
+    step(kt, sa, sb);
+    last(sb);
+  } else {
+    last(sa);
   }
   FA_WAIT_VM(0);
 
@@ -484,7 +514,7 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   // When every workgroup ends together (two-tile cross attention) the
   // fragment stores took several microseconds of the launch.
   const int ql = lane & 31;
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = fa_sum_halves(l_run);
   const float inv = 1.0f / l_tot;
   __syncthreads();  // every wave is done reading the K / V^T ring
   unsigned char DLM_LDS* ob = smem + wave * 4096;  // this wave's 32 rows x 128 B, chunks swizzled
