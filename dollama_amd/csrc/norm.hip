@@ -65,7 +65,8 @@ __device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
   v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
 }
 
-// partial[n][chunk][g] = (mean, M2) of group g over the chunk's pixels.
+// partial[n][g][chunk] = (mean, M2) of group g over the chunk's pixels (a
+// group's chunks contiguous, so the merge's lanes read consecutive partials).
 // Per-channel sums are shifted by the chunk's first pixel, reduced over the R
 // rows in LDS, turned into per-channel (mean, M2) and combined per group with
 // the equal-count form of Chan's formula.
@@ -156,7 +157,7 @@ __global__ void gn_partial_kernel(const T* __restrict__ a, int Ca, int lda,
       const float d = q.x - mean;
       m2 += q.y + cnt * d * d;
     }
-    partial[((size_t)n * chunks + ch) * G + g] = make_float2(mean, m2);
+    partial[((size_t)n * G + g) * chunks + ch] = make_float2(mean, m2);
   }
 }
 
@@ -185,10 +186,10 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
   const int n = blockIdx.x / G, g = blockIdx.x % G;
   const int lane = threadIdx.x;
   const int cpg = C / G;
-  const float2* pg = partial + (size_t)n * chunks * G + g;
+  const float2* pg = partial + ((size_t)n * G + g) * chunks;
   double cnt = 0.0, s1 = 0.0;
   for (int chn = lane; chn < chunks; chn += 64) {
-    const float2 q = pg[(size_t)chn * G];
+    const float2 q = pg[chn];
     const double nb = (double)(min(HW, (chn + 1) * chunk) - chn * chunk) * cpg;
     cnt += nb;
     s1 = fma(nb, (double)q.x, s1);
@@ -201,7 +202,7 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
   const double mean = cnt > 0.0 ? s1 / cnt : 0.0;
   double m2 = 0.0;
   for (int chn = lane; chn < chunks; chn += 64) {
-    const float2 q = pg[(size_t)chn * G];
+    const float2 q = pg[chn];
     const double nb = (double)(min(HW, (chn + 1) * chunk) - chn * chunk) * cpg;
     const double d = (double)q.x - mean;
     m2 += (double)q.y + nb * d * d;
