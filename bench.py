@@ -7,8 +7,10 @@ Prints one JSON line.  ``value`` is the mean device time of one full UNet step
 (ms, lower is better) over ``--steps`` timed forwards (HIP-graph replays)
 with all inputs resident in HBM.  Extra fields:
 - per kernel class and per kernel instantiation, time and algorithmic
-  TFLOP/s from device events around every launch of separately profiled
-  forwards (on the stream the kernels run on);
+  TFLOP/s from separately profiled forwards in which every launch carries a
+  device event pair in its own dispatch (hipExtLaunchKernel, on the stream
+  the kernel runs on), so the intervals are the kernels' execution without
+  marker packets between them;
 - ``roofline``: the single kernel instantiation with the most time, its
   algorithmic FLOPs per launch over its average launch duration against the
   fp16 MFMA peak, and its HBM bytes per launch from rocprofv3 PMC counters
@@ -374,17 +376,13 @@ def main():
     dom = max((n for n, k in kernels.items() if k["class"] in ("conv", "linear", "attention")),
               key=lambda n: kernels[n]["ms"])
     dk = kernels[dom]
-    bracketed_us = dk["ms"] / dk["launches"] * 1e3
-    # its average launch duration: the step's problems of this kernel replayed
-    # back to back (per-launch event pairs inside the forward add ~3 us each)
+    # its average launch duration inside the step: the dispatch-attached event
+    # pairs of its launches in the profiled forwards
+    dom_avg_us, dom_flop = dk["ms"] / dk["launches"] * 1e3, dk["flops"] / dk["launches"]
+    dom_timing = ("this kernel's launches in the profiled forwards, each carrying a device event pair in "
+                  "its own dispatch (hipExtLaunchKernel) on the stream it runs on")
+    # cross-check: the step's problems of this kernel replayed in isolation
     rp = replay_kernel(dom, kreports[-1][dom]["problems"], dev, args.seed + 3)
-    if rp is not None:
-        dom_avg_us, dom_flop = rp
-        dom_timing = ("the step's launches of this kernel (its GEMM problems, weighted by launches per "
-                      "step) captured into a HIP graph and replayed between device events")
-    else:
-        dom_avg_us, dom_flop = bracketed_us, dk["flops"] / dk["launches"]
-        dom_timing = "device events around each launch of the profiled forwards"
     achieved = dom_flop / (dom_avg_us * 1e-6) / 1e12
     traffic = measured_traffic().get(dom, {})
 
@@ -454,7 +452,7 @@ def main():
             "avg_launch_us": round(dom_avg_us, 2),
             "flop_per_launch": dom_flop,
             "timing": dom_timing,
-            "in_step_bracketed_avg_launch_us": round(bracketed_us, 2),
+            "replay_avg_launch_us": round(rp[0], 2) if rp is not None else None,
         },
         "kernels": {n: {kk: v for kk, v in k.items() if kk not in ("bytes", "problems")}
                     for n, k in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])[:12]},

@@ -89,6 +89,8 @@ HIP_SIGNATURES = {
     "dlm_event_record": (I, [P, P]),
     "dlm_event_synchronize": (I, [P]),
     "dlm_event_elapsed_ms": (I, [POINTER(c_float), P, P]),
+    "dlm_prof_arm": (I, [P, P]),
+    "dlm_prof_disarm": (I, []),
     "dlm_conv2d_fp16": (I, [P, P, P, P] + [I] * 13 + [P]),
     "dlm_gemm_fp16": (I, [P, P, P, I, I, I, F, F, I, I, P]),
     "dlm_group_norm_fp16": (I, [P, P, P, P, I, I, I, I, I, F, I, P]),

@@ -5,9 +5,13 @@
 // accumulation is always fp32.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
 #include <string>
+#include <tuple>
+#include <utility>
 
 #include "../../include/dlm.h"
 
@@ -104,12 +108,44 @@ void note_kernel(const char* name);
 // reduction length K, flags (bit 0 residual, bits 4.. epilogue activation,
 // bit 8 implicit-GEMM conv).
 void note_dims(int M, int N, int K, int flags);
+// Events armed by dlm_prof_arm on this thread (stop == nullptr: disarmed) and
+// the number of kernels launched since arming.
+struct ProfArm {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+  int launched = 0;
+};
+ProfArm& prof_arm();
+
+// Every kernel launch of the library.  The arguments are converted to the
+// kernel's parameter types and passed by address, as hipLaunchKernelGGL does;
+// while dispatch timing is armed the launch goes through hipExtLaunchKernel
+// with the armed events attached to this dispatch.
+template <typename... F, typename... A>
+inline void launch(void (*kernel)(F...), const dim3& grid, const dim3& block, uint32_t shmem,
+                   hipStream_t s, A&&... a) {
+  static_assert(sizeof...(F) == sizeof...(A), "kernel argument count mismatch");
+  std::tuple<F...> args{std::forward<A>(a)...};
+  std::apply(
+      [&](auto&... e) {
+        void* ptrs[] = {static_cast<void*>(&e)..., nullptr};
+        ProfArm& p = prof_arm();
+        if (p.stop) {
+          (void)hipExtLaunchKernel(reinterpret_cast<void*>(kernel), grid, block, ptrs, shmem, s,
+                                   p.launched == 0 ? p.start : nullptr, p.stop, 0);
+          ++p.launched;
+        } else {
+          (void)hipLaunchKernel(reinterpret_cast<void*>(kernel), grid, block, ptrs, shmem, s);
+        }
+      },
+      args);
+}
 }  // namespace dlm
 
 #define DLM_LAUNCH(name, ...)          \
   do {                                 \
     ::dlm::note_kernel(name);          \
-    hipLaunchKernelGGL(__VA_ARGS__);   \
+    ::dlm::launch(__VA_ARGS__);        \
   } while (0)
 
 #define DLM_HIP(expr)                                                          \

@@ -1572,7 +1572,7 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
       sp = SplitArgs{1, nk, nullptr, nullptr};
       note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, true, Desc>());
       note_dims(M, N, bd.K, dims_flags);
-      hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, true, Desc>), dim3(tiles), dim3(NT),
+      launch((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, true, Desc>), dim3(tiles), dim3(NT),
                          0, s, ad, bd, ep, tiles_m, tiles_n, sp);
       DLM_LAUNCH_CHECK();
       return DLM_OK;
@@ -1583,7 +1583,7 @@ static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   const int grid = sp.S > 1 ? 8 * ((tiles + 7) / 8) * sp.S : tiles;
   note_kernel(dma_kernel_name<BM, BN, WM, WN, NS, PF, SPS, false, Desc>());
   note_dims(M, N, bd.K, dims_flags);
-  hipLaunchKernelGGL((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, false, Desc>), dim3(grid), dim3(NT), 0,
+  launch((dma_gemm_kernel<BM, BN, WM, WN, NS, PF, SPS, false, Desc>), dim3(grid), dim3(NT), 0,
                      s, ad, bd, ep, tiles_m, tiles_n, sp);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
@@ -1597,7 +1597,7 @@ static int launch_cfg(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int 
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
   note_kernel(mfma_kernel_name<BM, BN, WM, WN, DEEP, Desc>());
   note_dims(M, N, bd.K, (ep.res ? 1 : 0) | (ep.act << 4) | (std::is_same<Desc, ConvDesc>::value ? 256 : 0));
-  hipLaunchKernelGGL((mfma_gemm_kernel<BM, BN, WM, WN, DEEP, Desc>), dim3(tiles_m * tiles_n),
+  launch((mfma_gemm_kernel<BM, BN, WM, WN, DEEP, Desc>), dim3(tiles_m * tiles_n),
                      dim3(NT), 0, s, ad, bd, ep, tiles_m, tiles_n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;

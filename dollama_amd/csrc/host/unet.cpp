@@ -12,11 +12,17 @@
 
 namespace dollama {
 
-// Launch one C-ABI kernel call, bracketed by profiling events when enabled.
+// Launch one C-ABI kernel call; when profiling, its kernels carry an event
+// pair in their own dispatches (dlm_prof_arm).
 #define LAUNCH(cls, flops, bytes, expr)          \
   do {                                           \
     prof_begin((cls), (flops), (bytes), stream); \
-    DLM_CALL(expr);                              \
+    try {                                        \
+      DLM_CALL(expr);                            \
+    } catch (...) {                              \
+      if (prof_on_) (void)dlm_prof_disarm();     \
+      throw;                                     \
+    }                                            \
     prof_end(stream);                            \
   } while (0)
 
@@ -277,12 +283,17 @@ void UNet::prof_begin(int cls, double flops, double bytes, void* stream) {
   if (prof_recs_.size() <= prof_next_) prof_recs_.resize(prof_next_ + 1);
   prof_recs_[prof_next_] = ProfRec{cls, flops, bytes, std::string(), {0, 0, 0, 0}};
   (void)dlm_last_kernel(1);
-  DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2], stream));
+  // the kernels of the call carry the event pair in their own dispatches
+  DLM_CALL(dlm_prof_arm(prof_events_[prof_next_ * 2], prof_events_[prof_next_ * 2 + 1]));
+  (void)stream;
 }
 
 void UNet::prof_end(void* stream) {
   if (!prof_on_) return;
-  DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2 + 1], stream));
+  if (dlm_prof_disarm() == 0) {  // no kernel in the call: an empty interval
+    DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2], stream));
+    DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2 + 1], stream));
+  }
   DLM_CALL(dlm_last_kernel_dims(prof_recs_[prof_next_].dims));
   prof_recs_[prof_next_].kernel = dlm_last_kernel(1);
   ++prof_next_;

@@ -15,7 +15,12 @@ namespace dollama {
 #define LAUNCH(cls, flops, bytes, expr)          \
   do {                                           \
     prof_begin((cls), (flops), (bytes), stream); \
-    DLM_CALL(expr);                              \
+    try {                                        \
+      DLM_CALL(expr);                            \
+    } catch (...) {                              \
+      if (prof_on_) (void)dlm_prof_disarm();     \
+      throw;                                     \
+    }                                            \
     prof_end(stream);                            \
   } while (0)
 
@@ -119,12 +124,17 @@ void VAE::prof_begin(int cls, double flops, double bytes, void* stream) {
   }
   if (prof_recs_.size() <= prof_next_) prof_recs_.resize(prof_next_ + 1);
   prof_recs_[prof_next_] = ProfRec{cls, flops, bytes};
-  DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2], stream));
+  // the kernels of the call carry the event pair in their own dispatches
+  DLM_CALL(dlm_prof_arm(prof_events_[prof_next_ * 2], prof_events_[prof_next_ * 2 + 1]));
+  (void)stream;
 }
 
 void VAE::prof_end(void* stream) {
   if (!prof_on_) return;
-  DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2 + 1], stream));
+  if (dlm_prof_disarm() == 0) {  // no kernel in the call: an empty interval
+    DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2], stream));
+    DLM_CALL(dlm_event_record(prof_events_[prof_next_ * 2 + 1], stream));
+  }
   ++prof_next_;
 }
 

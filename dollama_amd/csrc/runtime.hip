@@ -32,6 +32,11 @@ void note_dims(int M, int N, int K, int flags) {
   g_last_dims[3] = flags;
 }
 
+ProfArm& prof_arm() {
+  static thread_local ProfArm a;
+  return a;
+}
+
 void set_error(const std::string& msg) { g_last_error = msg; }
 
 int fail(int code, const std::string& msg) {
@@ -102,6 +107,22 @@ const char* dlm_last_kernel(int reset) {
   const char* k = dlm::g_last_kernel;
   if (reset) dlm::note_kernel("");
   return k;
+}
+
+int dlm_prof_arm(void* start, void* stop) {
+  DLM_REQUIRE(start != nullptr && stop != nullptr, "start / stop event is NULL");
+  dlm::ProfArm& p = dlm::prof_arm();
+  p.start = (hipEvent_t)start;
+  p.stop = (hipEvent_t)stop;
+  p.launched = 0;
+  return DLM_OK;
+}
+
+int dlm_prof_disarm(void) {
+  dlm::ProfArm& p = dlm::prof_arm();
+  const int n = p.launched;
+  p = dlm::ProfArm{};
+  return n;
 }
 
 int dlm_last_kernel_dims(int* dims) {

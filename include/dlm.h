@@ -59,6 +59,18 @@ const char* dlm_last_kernel(int reset);
  * epilogue; bits 4-7: activation code; bit 8: conv; bit 9: LayerNorm folded
  * in, dlm_linear_ln_fp16); zeros otherwise. */
 int dlm_last_kernel_dims(int* dims);
+/* Dispatch timing, for a caller that times each entry-point call (no
+ * reference counterpart: the reference times its kernels with an external
+ * profiler).  While armed on this thread, every kernel the library launches
+ * carries the two events in its own dispatch (hipExtLaunchKernel): `start`
+ * takes the start of the first launch after arming, `stop` the end of each
+ * launch.  The pair then spans the kernels of the calls made while armed with
+ * no marker packets between them, i.e. the kernels' own execution as a
+ * profiler's kernel trace reports it.  dlm_prof_disarm returns how many
+ * kernels were launched while armed (0: the events were not touched).  Not
+ * for work being captured into a graph. */
+int dlm_prof_arm(void* start, void* stop);
+int dlm_prof_disarm(void);
 int dlm_get_device_count(int* count);
 int dlm_set_device(int device);
 /* Name of the GPU architecture of the current device (e.g. "gfx950"). */
