@@ -58,3 +58,16 @@ def test_host_library_pure_host_entry_points():
     assert specs["conv_in.weight"] == (320, 4, 3, 3)
     sig, ts = U.euler_schedule(20)
     assert len(sig) == 21 and ts[0] == 951.0 and ts[-1] == 1.0
+
+
+def test_dispatch_timing_arm_contract_without_a_device():
+    lib = ctypes.CDLL(LIBS["dlm.h"])
+    lib.dlm_prof_arm.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    # both events are required
+    assert lib.dlm_prof_arm(None, None) == 1  # DLM_ERR_INVALID_ARG
+    # disarming when nothing is armed, or after an arm with no launch, reports 0 kernels
+    assert lib.dlm_prof_disarm() == 0
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: no kernel is launched while armed
+    assert lib.dlm_prof_arm(fake, fake) == 0
+    assert lib.dlm_prof_disarm() == 0
+    assert lib.dlm_prof_disarm() == 0

@@ -113,6 +113,66 @@ def test_unet_layernorm_fold_matches_unfolded(gpu):
     net.close()
 
 
+def test_unet_profiled_forward_times_each_kernel(gpu):
+    """Profiling attaches a device event pair to each call's kernels in their
+    own dispatches (dlm_prof_arm): the profiled forward equals the plain eager
+    forward bit for bit, every class that ran is timed, the per-kernel report
+    adds up to the per-class report, and the kernels' time fits inside the
+    forward's own device time.  At the C ABI, an armed pair spans the kernels
+    of one call and disarming reports how many were launched."""
+    cfg = TINY
+    print("[case] tiny UNet profiled forward (dispatch-attached events)", flush=True)
+    Wc = OR.random_weights(OR.TINY, seed=23)
+    lat, ts, ehs, text, ids = _inputs(cfg, 2, 32, 32, 77, seed=24)
+    net = U.UNet(cfg)
+    net.set_weights(_to_gpu(Wc))
+    net.prepare()
+    args = (lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
+    ref = net.forward(*args).float()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    net.forward(*args)
+    e1.record()
+    torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1)
+    net.set_profiling(True)
+    got = net.forward(*args).float()
+    torch.cuda.synchronize()
+    rep, ker = net.profile_report(), net.profile_kernels()
+    net.set_profiling(False)
+    assert torch.equal(got, ref), "profiled forward differs from the plain eager forward"
+    for c in ("conv", "linear", "attention", "groupnorm", "layernorm"):
+        assert rep[c]["launches"] > 0 and rep[c]["ms"] > 0.0, c
+    cls_ms = sum(v["ms"] for v in rep.values())
+    ker_ms = sum(k["ms"] for k in ker.values())
+    assert sum(v["launches"] for v in rep.values()) == sum(k["launches"] for k in ker.values())
+    assert abs(cls_ms - ker_ms) <= 1e-3 * cls_ms + 1e-4, (cls_ms, ker_ms)
+    assert 0.0 < cls_ms <= 1.05 * fwd_ms + 0.05, (cls_ms, fwd_ms)
+    net.close()
+
+    from dollama_amd import ops
+    lib = U._lib
+    ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in ev:
+        lib.call("dlm_event_create", ctypes.byref(e))
+    x = torch.randn(2048, 1280, device="cuda").half()
+    w = (torch.randn(1280, 1280, device="cuda") * 0.02).half()
+    y = torch.empty(2048, 1280, device="cuda").half()
+    ops.linear(x, w, out=y)
+    torch.cuda.synchronize()
+    lib.call("dlm_prof_arm", ev[0], ev[1])
+    ops.linear(x, w, out=y)
+    n = lib.hip_lib().dlm_prof_disarm()
+    assert n == 1, n
+    torch.cuda.synchronize()
+    ms = ctypes.c_float()
+    lib.call("dlm_event_elapsed_ms", ctypes.byref(ms), ev[0], ev[1])
+    assert 0.0 < ms.value < 10.0, ms.value
+    assert lib.hip_lib().dlm_prof_disarm() == 0
+    for e in ev:
+        lib.call("dlm_event_destroy", e)
+
+
 def test_unet_batch2_equals_two_batch1(gpu):
     cfg = TINY
     H = W = 32
