@@ -1,4 +1,5 @@
-"""Block-level parity at the SDXL widths (BASELINE configs 2 and 4), through
+"""Block-level parity at the SDXL widths (the ResnetBlock2D and
+BasicTransformerBlock benchmark shapes), through
 the prepared UNet's block runners (the same code the forward runs), against
 the fp32 CPU oracle's resnet_block / transformer_block
 (oracle/unet_ref.py, restating src/infer/unet.cu:537-797).
