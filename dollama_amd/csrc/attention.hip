@@ -454,24 +454,28 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 
-  // one tile: sc holds its scores, the next tile's scores go to sn
-  int cur = 0;
-  auto step = [&](int kt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-    const int nxt = cur == FA_NS - 1 ? 0 : cur + 1;
+  // one tile at ring position c: sc holds its scores, the next tile's
+  // scores go to sn
+  auto body = [&](int kt, int c, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    const int nxt = c == FA_NS - 1 ? 0 : c + 1;
     const int nn = nxt == FA_NS - 1 ? 0 : nxt + 1;
     FA_WAIT_VM(0);  // tile kt+1 (this wave's part)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 2 < nkt) issue(nn, kt + 2);
-    const unsigned char DLM_LDS* st = smem + cur * FA_STAGE;
+    const unsigned char DLM_LDS* st = smem + c * FA_STAGE;
     scores(smem + nxt * FA_STAGE, sn);  // tile kt+1, in the shadow of the softmax below
     f16x8 vf[8];
     vread(st, vf);
     f16x8 pf[4];
     softmax(sc, pf);  // tiles before the last are full: no mask
     pv(vf, pf);
-    cur = nxt;
+  };
+  int cur = 0;  // ring position of the current tile
+  auto step = [&](int kt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    body(kt, cur, sc, sn);
+    cur = cur == FA_NS - 1 ? 0 : cur + 1;
   };
   // last tile: its keys may end inside the tile
   auto last = [&](f32x16 (&sc)[2]) {
@@ -496,6 +500,17 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   f32x16 sa[2], sb[2];
   scores(smem, sa);
   int kt = 0;
+  // six tiles per iteration: the ring position and the score buffers both
+  // come back to where they started, so every LDS address in the body is a
+  // constant offset from one base
+  for (; kt + 6 < nkt; kt += 6) {
+    body(kt, 0, sa, sb);
+    body(kt + 1, 1, sb, sa);
+    body(kt + 2, 2, sa, sb);
+    body(kt + 3, 0, sb, sa);
+    body(kt + 4, 1, sa, sb);
+    body(kt + 5, 2, sb, sa);
+  }
   for (; kt + 2 < nkt; kt += 2) {
     step(kt, sa, sb);
     step(kt + 1, sb, sa);
