@@ -345,7 +345,7 @@ def main():
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite noise_pred")
 
-    # per-class and per-kernel time from device events around every launch
+    # per-class and per-kernel time from device events attached to every launch's own dispatch
     net.set_profiling(True)
     reports, kreports = [], []
     for _ in range(max(1, args.profile_runs)):
