@@ -19,9 +19,10 @@ with all inputs resident in HBM.  Extra fields:
   3x3 conv, three ResnetBlock2D shapes, the two self-attention shapes, one
   BasicTransformerBlock);
 - a 20-step CFG Euler loop on the device;
-- ``cpu_baseline``: the fp32 CPU oracle running one full step of the same
-  workload (same weights and inputs) on this host, with its noise_pred
-  compared against the GPU's.
+- ``cpu_baseline``: the fp32 CPU oracle running full steps of the same
+  workload (same weights and inputs) on this host, median of 3, with its
+  noise_pred compared against the GPU's; each ``configs`` entry carries the
+  oracle's time for that configuration (``cpu_ms``, median of 5).
 """
 import argparse
 import json
@@ -81,6 +82,12 @@ def measured_traffic():
         return json.load(f).get("kernels", {})
 
 
+def _progress(msg):
+    """One progress line on stderr per phase (the JSON line stays alone on
+    stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -92,35 +99,98 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(w_cpu, inputs, gpu_out):
-    """One full UNet step of the same workload (same weights, same fp16 inputs)
-    through the fp32 torch-CPU oracle on this host's CPU share, after a warm-up
-    forward on a 32x32 latent; the oracle's noise_pred is compared with the
-    GPU's (SSIM of the reference's definition, relative error)."""
+def _cpu_threads():
+    import torch
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _median_s(fn, runs, warmup=1):
+    """Median wall time (s) of fn() over `runs` calls after `warmup` calls."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], ts
+
+
+def cpu_baseline(w_cpu, inputs, gpu_out, runs=3):
+    """Full UNet steps of the same workload (same weights, same fp16 inputs)
+    through the fp32 torch-CPU oracle on this host's CPU share: one warm-up
+    forward on a 32x32 latent, then `runs` full steps, median reported.  The
+    oracle's noise_pred is compared with the GPU's (SSIM of the reference's
+    definition, relative error, cosine)."""
     import torch
     from oracle import metrics
     from oracle import unet_ref as OR
-    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    threads = _cpu_threads()
     lat, ts, ehs, text, ids = inputs
     OR.unet_forward(w_cpu, OR.SDXL, lat[:, :, :32, :32].contiguous(), ts, ehs, text, ids)
-    t0 = time.perf_counter()
-    ref = OR.unet_forward(w_cpu, OR.SDXL, lat, ts, ehs, text, ids)
-    sec = time.perf_counter() - t0
+    box = {}
+
+    def step():
+        t0 = time.perf_counter()
+        box["ref"] = OR.unet_forward(w_cpu, OR.SDXL, lat, ts, ehs, text, ids)
+        _progress(f"CPU oracle step {time.perf_counter() - t0:.1f} s")
+
+    med, all_s = _median_s(step, runs, warmup=0)
+    ref = box["ref"]
     got = gpu_out.float().cpu()
     return {
-        "value": round(sec * 1e3, 1),
+        "value": round(med * 1e3, 1),
         "unit": "ms/step",
         "cores": threads,
         "kind": "port",
-        "sample": "one full SDXL UNet step (B=2, latent 128x128, ctx 77x2048) through the fp32 "
-                  "torch-CPU oracle with the GPU run's weights and inputs, after a 32x32 warm-up",
+        "runs": runs,
+        "runs_ms": [round(t * 1e3, 1) for t in all_s],
+        "sample": f"median of {runs} full SDXL UNet steps (B=2, latent 128x128, ctx 77x2048) through the "
+                  "fp32 torch-CPU oracle with the GPU run's weights and inputs, after a 32x32 warm-up",
         "cpu_model": cpu_model(),
         "host_logical_cpus": os.cpu_count(),
         "gpu_vs_cpu": {"ssim": round(metrics.ssim_uniform(got, ref), 7),
                        "rel_err": float(f"{metrics.rel_err(got, ref):.3e}"),
                        "cosine": round(metrics.cosine(got, ref), 7)},
     }
+
+
+def cpu_config_timings(w_cpu, seed, runs=5):
+    """The benchmark's configurations 1-4 on the fp32 torch-CPU oracle (one
+    warm-up, median of `runs`), same shapes as config_timings: ms per call,
+    keyed like its entries."""
+    import torch
+    from oracle import ref_ops as R
+    from oracle import unet_ref as OR
+    _cpu_threads()
+    g = torch.Generator().manual_seed(seed)
+
+    def rn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g) * std).half().float()
+
+    out = {}
+    x = rn(1, 320, 128, 128)
+    w, b = rn(320, 320, 3, 3, std=0.02), rn(320, std=0.01)
+    out["conv3x3_320_128px_n1_bias_silu"] = _median_s(lambda: R.silu(R.conv2d(x, w, b, 1, 1)), runs)[0]
+    temb = R.silu(rn(2, 1280))
+    for name, prefix, ci, hw in (("resnet_640ch_64px", "down_blocks.1.resnets.1.", 640, 64),
+                                 ("resnet_1280ch_32px", "mid_block.resnets.0.", 1280, 32),
+                                 ("resnet_320to640_64px_1x1skip", "down_blocks.1.resnets.0.", 320, 64)):
+        xr = rn(2, ci, hw, hw)
+        out[name] = _median_s(lambda: OR.resnet_block(w_cpu, prefix, xr, temb), runs)[0]
+    for name, B, H, S in (("attention_b2_h10_s4096", 2, 10, 4096), ("attention_b2_h20_s1024", 2, 20, 1024)):
+        q, k, v = rn(B, H, S, 64), rn(B, H, S, 64), rn(B, H, S, 64)
+        out[name] = _median_s(lambda: R.attention(q, k, v, 0.125), runs)[0]
+    xt, ctx = rn(2, 4096, 640), rn(2, 77, 2048)
+    out["basic_transformer_block_2x4096x640"] = _median_s(
+        lambda: OR.transformer_block(w_cpu, "down_blocks.1.attentions.0.transformer_blocks.0.", xt, ctx, 10),
+        runs)[0]
+    # the reference-layout entries compute the same functions on the same shapes
+    out["reference_layout_conv2d_nchw_320_128px_n1_bias"] = out["conv3x3_320_128px_n1_bias_silu"]
+    out["reference_layout_attention_b2_h10_s4096"] = out["attention_b2_h10_s4096"]
+    return {k: round(v * 1e3, 2) for k, v in out.items()}
 
 
 def queue_ahead(seconds=0.01):
@@ -333,6 +403,7 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps, (time.perf_counter() - w0) / args.steps * 1e3
 
+    _progress("setup done, timing eager forwards")
     eager_ms, eager_wall = timed(False)
     eager_out = out.clone()
     if args.eager:
@@ -345,6 +416,7 @@ def main():
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite noise_pred")
 
+    _progress(f"step {ms:.3f} ms (eager {eager_ms:.3f} ms); profiling forwards")
     # per-class and per-kernel time from device events attached to every launch's own dispatch
     net.set_profiling(True)
     reports, kreports = [], []
@@ -386,6 +458,7 @@ def main():
     achieved = dom_flop / (dom_avg_us * 1e-6) / 1e12
     traffic = measured_traffic().get(dom, {})
 
+    _progress("profiled; Euler loop")
     # 20-step CFG Euler denoise loop on the device
     loop = None
     if args.loop_steps > 0:
@@ -403,12 +476,21 @@ def main():
                 "finite": bool(torch.isfinite(lt).all()), "graphs": not args.eager}
         net.set_graphs(False)
 
+    _progress("per-config timings")
     configs = None if args.no_configs else config_timings(net, U, dev, args.seed + 2)
 
     cpu = None
     if w_cpu is not None:
+        if configs is not None:
+            _progress("CPU oracle legs of configurations 1-4 (median of 5 each)")
+            cpu_ms = cpu_config_timings(w_cpu, args.seed + 4)
+            for name, c in configs.items():
+                c["cpu_ms"] = cpu_ms.get(name)
+                c["gpu_vs_cpu"] = round(cpu_ms[name] / c["ms"], 1) if name in cpu_ms else None
         inputs = (latent.float().cpu(), ts.cpu(), ehs.float().cpu(), text.float().cpu(), ids.float().cpu())
+        _progress("CPU oracle full steps (median of 3)")
         cpu = cpu_baseline(w_cpu, inputs, eager_out)
+        cpu["configs_runs"] = 5 if configs is not None else None
         del w_cpu
 
     line = {

@@ -123,6 +123,7 @@ HIP_SIGNATURES = {
     "dlm_sdxl_embed_inputs_fp16": (I, [P, P, I, P, I, I, P, I, P, I, P]),
     "dlm_linear_small_fp16": (I, [P, I, P, P, P, I, I, I, I, I, I, I, P]),
     "dlm_euler_cfg_step": (I, [P, P, P, I, F, F, F, F, P]),
+    "dlm_euler_step": (I, [P, P, P, I, F, F, F, P]),
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),
     "dlm_linear_f32out_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, F, F, I, P]),
     "dlm_group_norm_nhwc_f32in": (I, [P, I, P, P, P, I, I, I, I, I, F, I, P, P]),

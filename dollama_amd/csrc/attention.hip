@@ -6,17 +6,22 @@
 // which compute O = softmax(scale * Q K^T) V with fp32 softmax over 16-row
 // warp tiles.
 //
-// Layout of the computation (wave64, v_mfma_f32_32x32x16_f16):
-//   * each wave owns 32 queries, a workgroup 4 waves (128 queries) of one
-//     (batch, head); K/V tiles of 64 keys are double-buffered in LDS, K as
-//     [key][d], V transposed to [d][key] while staging;
+// Two kernels share one formulation (wave64, v_mfma_f32_32x32x16_f16):
 //   * scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q held
-//     in registers), so a lane owns one query and 16 of its keys: the row
-//     max needs one exchange with the lane 32 apart, not a 32-lane reduction;
+//     in registers), so a lane owns one query and 16 of its keys per 32-key
+//     block: the row max needs one exchange with the lane 32 apart, not a
+//     32-lane reduction;
 //   * the exponentiated scores stay in registers and feed O^T = V^T P^T
 //     directly as the B operand (the key order inside a 16-key step is a
 //     fixed permutation shared by both operands), so the output accumulator
 //     is also lane-per-query and the online-softmax rescale is per lane.
+// flash_vt_pipe_kernel (the UNet's self and cross attention) reads a
+// transposed V, DMAs K and V^T tiles into a three-tile LDS ring and
+// software-pipelines each tile's scores under the previous tile's softmax;
+// it is described at its definition.  flash_attn_d64_kernel (the strided
+// entry dlm_attention_strided_fp16, V as [key][d]) uses 4 waves of 32 queries per
+// workgroup and double-buffered K / V tiles staged through VGPRs, V
+// transposed to [d][key] while staging.
 // Q, K, V and O are addressed with independent batch / token / head strides,
 // so the fused QKV projection output [B, S, 3C] is read in place.
 #include <algorithm>
@@ -578,6 +583,9 @@ int attention_vt(const dlm_attention_vt_args* a, hipStream_t s) {
   // workgroups, whose one K/V staging serves twice the queries.
   p.H = a->H;
   p.B = a->B;
+  // the 1-D grid counts query blocks x heads x batch in int (host and kernel)
+  if ((long long)((a->Sq + 63) / 64) * a->H * a->B >= (1LL << 31))
+    return fail(DLM_ERR_UNSUPPORTED, "attention: more than 2^31 query blocks x heads x batch");
   if (a->Sk > 2 * FA_TK && (long long)((a->Sq + 127) / 128) * a->H * a->B < 512) {
     p.nqb = (a->Sq + 63) / 64;
     DLM_LAUNCH("flash_vt_pipe_kernel<2>", flash_vt_pipe_kernel<2>, dim3(p.nqb * p.H * p.B), dim3(128), 0, s, p);

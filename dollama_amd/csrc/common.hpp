@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include <string>
 #include <tuple>
 #include <utility>
@@ -87,6 +89,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Grid of a grid-stride elementwise launch over n items.
+static inline int grid_for(long long n, int threads = 256, int cap = 8192) {
+  return (int)std::max<long long>(1, std::min<long long>((n + threads - 1) / threads, cap));
+}
+
+#define GRID_STRIDE(i, n)                                                          \
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < (n); \
+       i += (long long)gridDim.x * blockDim.x)
+
 }  // namespace dlm
 
 // ---------------------------------------------------------------------------
@@ -101,6 +112,10 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line);
 // frees the old block, so those entry points are not capturable into a graph
 // until their slots have reached size.
 void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status);
+int scratch_release(hipStream_t stream);
+size_t scratch_bytes();
+int split_workspace_release(hipStream_t stream);
+size_t split_workspace_bytes();
 // Name of the kernel an entry point launches last (per thread), for
 // per-kernel timing attribution (dlm_last_kernel).
 void note_kernel(const char* name);

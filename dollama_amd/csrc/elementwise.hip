@@ -19,14 +19,6 @@
 
 namespace dlm {
 
-static inline int grid_for(long long n, int threads = 256, int cap = 8192) {
-  return (int)std::max<long long>(1, std::min<long long>((n + threads - 1) / threads, cap));
-}
-
-#define GRID_STRIDE(i, n)                                                          \
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < (n); \
-       i += (long long)gridDim.x * blockDim.x)
-
 __global__ void silu_kernel(const f16* in, f16* out, long long n) {
   GRID_STRIDE(i, n) out[i] = (f16)silu_f((float)in[i]);
 }

@@ -12,11 +12,21 @@
 //     (src/kernels/bias_add.cu:106-159) as conv epilogues.
 //
 // Design: C[M,N] = A[M,K] * W[N,K]^T with both operands K-contiguous, the
-// form MFMA consumes directly.  A workgroup owns a BM x BN output tile and 4
-// waves; each wave owns WM x WN built from 32x32 MFMA blocks.  K advances in
-// 64-wide slices staged in double-buffered LDS (row stride 72 halfs, which
-// puts the 8 rows a ds_read_b128 phase touches on distinct banks); the next
-// slice's global loads are issued before the current slice's MFMAs.
+// form MFMA consumes directly.  Two kernels:
+//   - dma_gemm_kernel (every aligned UNet / VAE shape): a BM x BN tile per
+//     workgroup of 8 waves, each wave a WM x WN block of
+//     v_mfma_f32_16x16x32_f16 tiles in transposed form (W fragment x A
+//     fragment), so a lane holds one output row and 4 consecutive columns.
+//     K advances in 64-wide slices copied global -> LDS by DMA
+//     (buffer_load ... lds) into a ring of NS stages (one or two slices
+//     each, one barrier per stage); LDS rows are 128 B with their 16-byte
+//     chunks XOR-swizzled by (row >> 1) & 7, so every ds_read_b128 fragment
+//     phase is conflict-free; the next k-step's fragments are read before
+//     the current k-step's MFMAs.  Optional split-K with a last-arriver
+//     reduction in split order, and an XCD-aware tile order.
+//   - mfma_gemm_kernel (small channel counts, small grids, unaligned
+//     operands): 4 waves of 32x32x16 MFMA blocks with VGPR-staged,
+//     double-buffered LDS slices (row stride 72 halfs).
 // The A operand is produced by a loader: plain rows for linears, or the
 // implicit im2col gather (zero padding, channel concatenation of two
 // sources, nearest-2x upsampling, a second 1x1 segment) for convolutions.
@@ -28,6 +38,7 @@
 #include <utility>
 
 #include "common.hpp"
+#include "dlm_tuning.h"
 
 namespace dlm {
 
@@ -1498,6 +1509,36 @@ static const SplitWorkspace* split_workspace(hipStream_t s) {
   return &w;
 }
 
+// Frees the split-K workspace of `s` on every device (after synchronising
+// the stream).  Explicit only: a graph captured on a stream holds its
+// workspace's address, so nothing frees it behind the caller's back.
+int split_workspace_release(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_split_mu);
+  bool any = false;
+  for (const auto& kv : g_split_ws) any |= kv.first.second == s;
+  if (!any) return DLM_OK;
+  if (hipStreamSynchronize(s) != hipSuccess) return fail(DLM_ERR_HIP, "split workspace: stream synchronisation failed");
+  for (auto it = g_split_ws.begin(); it != g_split_ws.end();) {
+    if (it->first.second == s) {
+      if ((it->second.ws && hipFree(it->second.ws) != hipSuccess) ||
+          (it->second.cnt && hipFree(it->second.cnt) != hipSuccess))
+        return fail(DLM_ERR_HIP, "split workspace: hipFree failed");
+      it = g_split_ws.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return DLM_OK;
+}
+
+size_t split_workspace_bytes() {
+  std::lock_guard<std::mutex> lk(g_split_mu);
+  size_t t = 0;
+  for (const auto& kv : g_split_ws)
+    if (kv.second.ws) t += kSplitWsFloats * sizeof(float) + kSplitCounters * sizeof(int);
+  return t;
+}
+
 // Tuning aids (dlm_gemm_force_split / _set_variant / _force_tile /
 // _override_shape): thread-local, so they steer only launches made by the
 // thread that set them.
@@ -1965,10 +2006,12 @@ __global__ void geglu_pack_kernel(const f16* __restrict__ w, const f16* __restri
   if (threadIdx.x == 0 && b && bo) bo[r] = b[src];
 }
 
-// [rows, cols] -> [cols, rows] plain transpose used to bring operands of
-// dlm_gemm_fp16 into K-contiguous form.
+// [rows, cols] -> [cols, rows_pad] transpose used to bring operands of
+// dlm_gemm_fp16 into K-contiguous form: out[c * ld_out + r] = in[r][c] for
+// r < rows and 0 for rows <= r < rows_pad (the K padding), so the whole
+// destination is written by the kernel and no clearing pass is needed.
 __global__ void transpose_kernel(const f16* __restrict__ in, f16* __restrict__ out, int rows,
-                                 int cols, int ld_out) {
+                                 int cols, int ld_out, int rows_pad) {
   __shared__ f16 tile[32][33];
   const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
   const int tx = threadIdx.x, ty = threadIdx.y;
@@ -1979,7 +2022,19 @@ __global__ void transpose_kernel(const f16* __restrict__ in, f16* __restrict__ o
   __syncthreads();
   for (int r = ty; r < 32; r += 8) {
     const int cc = c0 + r, rr = r0 + tx;
-    if (cc < cols && rr < rows) out[(size_t)cc * ld_out + rr] = tile[tx][r];
+    if (cc < cols && rr < rows_pad) out[(size_t)cc * ld_out + rr] = tile[tx][r];
+  }
+}
+
+// out[r * ld_out + k] = in[r * ld_in + k] for k < K, 0 for K <= k < ld_out
+// (rows of an operand copied to an aligned, zero-padded row stride).
+__global__ void pad_k_kernel(const f16* __restrict__ in, int ld_in, f16* __restrict__ out,
+                                int ld_out, int rows, int K) {
+  const long long n = (long long)rows * ld_out;
+  GRID_STRIDE(i, n) {
+    const long long r = i / ld_out;
+    const int k = (int)(i - r * ld_out);
+    out[i] = k < K ? in[r * ld_in + k] : (f16)0.0f;
   }
 }
 
@@ -2023,9 +2078,11 @@ int conv_weight_pack(const void* w, void* out, int Cout, int Cin, int KH, int KW
 // fp16(W[n] * gamma) (gamma absent: a copy), c1[n] = sum_k W_out[n][k] (of the
 // rounded values), c2[n] = sum_k beta[k] W[n][k] + bias[n], both in fp32.
 // One 256-thread block per row; fixed-order reduction (deterministic).
-__global__ void ln_fold_kernel(const f16* __restrict__ w, int ldw, int K,
+// w and wo may be the same rows (in-place fold, ldo == ldw): each element is
+// read and then written by the same thread, so they carry no __restrict__.
+__global__ void ln_fold_kernel(const f16* w, int ldw, int K,
                                const f16* __restrict__ gamma, const f16* __restrict__ beta,
-                               const f16* __restrict__ bias, f16* __restrict__ wo, int ldo,
+                               const f16* __restrict__ bias, f16* wo, int ldo,
                                float* __restrict__ c1, float* __restrict__ c2) {
   const int n = blockIdx.x, tid = threadIdx.x;
   const f16* wr = w + (size_t)n * ldw;
@@ -2276,6 +2333,14 @@ int dlm_ln_fold_fp16(const void* W, int ldw, int N, int K, const void* gamma, co
   if (N <= 0 || K <= 0) return DLM_OK;
   DLM_REQUIRE(W && W_out && c1 && c2, "NULL operand");
   DLM_REQUIRE(ldw >= K && ldo >= K, "ldw/ldo smaller than K");
+  // in place only row for row: any other overlap of W and W_out would let one
+  // block overwrite rows another block still reads
+  const char* w0 = (const char*)W;
+  const char* w1 = w0 + ((size_t)(N - 1) * ldw + K) * 2;
+  const char* o0 = (const char*)W_out;
+  const char* o1 = o0 + ((size_t)(N - 1) * ldo + K) * 2;
+  if (o0 < w1 && w0 < o1)
+    DLM_REQUIRE(W_out == W && ldo == ldw, "W_out overlaps W: only the exact in-place fold (W_out == W, ldo == ldw) is allowed");
   return ln_fold(W, ldw, N, K, gamma, beta, bias, W_out, ldo, c1, c2, (hipStream_t)stream);
 }
 
@@ -2291,33 +2356,33 @@ int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K, fl
   const f16* b_ptr = (const f16*)B;
   int lda = K, ldb = K;
   int st = DLM_OK;
+  // The scratch copy is written whole by one kernel (values, then the zero K
+  // padding): no clearing pass.
   if (transA || Kp != K || !dlm_aligned16(A)) {
     f16* t = (f16*)scratch_slot((size_t)M * Kp * 2, 0, s, &st);
     if (!t) return st;
-    DLM_HIP(hipMemsetAsync(t, 0, (size_t)M * Kp * 2, s));
     if (transA) {  // A stored [K, M]
-      DLM_LAUNCH("transpose_kernel", transpose_kernel, dim3((M + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
-                         (const f16*)A, t, K, M, Kp);
-      DLM_LAUNCH_CHECK();
+      DLM_LAUNCH("transpose_kernel", transpose_kernel, dim3((M + 31) / 32, (Kp + 31) / 32), dim3(32, 8), 0, s,
+                 (const f16*)A, t, K, M, Kp, Kp);
     } else {
-      DLM_HIP(hipMemcpy2DAsync(t, (size_t)Kp * 2, A, (size_t)K * 2, (size_t)K * 2, M,
-                               hipMemcpyDeviceToDevice, s));
+      DLM_LAUNCH("pad_k_kernel", pad_k_kernel, dim3(grid_for((long long)M * Kp)), dim3(256), 0, s,
+                 (const f16*)A, K, t, Kp, M, K);
     }
+    DLM_LAUNCH_CHECK();
     a_ptr = t;
     lda = Kp;
   }
   if (!transB || Kp != K || !dlm_aligned16(B)) {
     f16* t = (f16*)scratch_slot((size_t)N * Kp * 2, 1, s, &st);
     if (!t) return st;
-    DLM_HIP(hipMemsetAsync(t, 0, (size_t)N * Kp * 2, s));
     if (!transB) {  // B stored [K, N]
-      DLM_LAUNCH("transpose_kernel", transpose_kernel, dim3((N + 31) / 32, (K + 31) / 32), dim3(32, 8), 0, s,
-                         (const f16*)B, t, K, N, Kp);
-      DLM_LAUNCH_CHECK();
+      DLM_LAUNCH("transpose_kernel", transpose_kernel, dim3((N + 31) / 32, (Kp + 31) / 32), dim3(32, 8), 0, s,
+                 (const f16*)B, t, K, N, Kp, Kp);
     } else {
-      DLM_HIP(hipMemcpy2DAsync(t, (size_t)Kp * 2, B, (size_t)K * 2, (size_t)K * 2, N,
-                               hipMemcpyDeviceToDevice, s));
+      DLM_LAUNCH("pad_k_kernel", pad_k_kernel, dim3(grid_for((long long)N * Kp)), dim3(256), 0, s,
+                 (const f16*)B, K, t, Kp, N, K);
     }
+    DLM_LAUNCH_CHECK();
     b_ptr = t;
     ldb = Kp;
   }

@@ -654,7 +654,7 @@ int dlm_st_info(void* handle, const char* name, int* dtype, int* ndim, int64_t* 
   return guarded([&] {
     if (!handle || !name || !dtype || !ndim || !shape || !nbytes) throw std::invalid_argument("NULL argument");
     const SafeTensors& st = *static_cast<SafeTensors*>(handle);
-    if (!st.has(name)) throw std::out_of_range(std::string("safetensors: no tensor '") + name + "'");
+    if (!st.contains(name)) throw std::out_of_range(std::string("safetensors: no tensor '") + name + "'");
     *dtype = (int)st.dtype(name);
     const auto& sh = st.shape(name);
     if (sh.size() > 8) throw std::invalid_argument("more than 8 dimensions");

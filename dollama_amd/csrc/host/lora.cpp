@@ -165,8 +165,8 @@ std::vector<LoraModule> load_lora_modules(const std::vector<WeightSpec>& base,
     if (hit == index.end())
       throw std::runtime_error("lora: module 'lora_unet_" + mod + "' matches no UNet weight");
     const WeightSpec& w = *hit->second;
-    const std::vector<int64_t>& as = lora.shape(g.down);
-    const std::vector<int64_t>& bs = lora.shape(g.up);
+    const std::vector<int64_t>& as = lora.shape_i64(g.down);
+    const std::vector<int64_t>& bs = lora.shape_i64(g.up);
     if (as.empty() || bs.empty()) throw std::runtime_error("lora: module '" + mod + "' has an empty shape");
     const int64_t rank = as[0], in_flat = tail(as), out_dim = bs[0];
     if (tail(bs) != rank)
@@ -198,17 +198,21 @@ void unet_apply_lora_file(UNet& u, const std::string& path, float strength, Lora
   SafeTensors st(path);
   LoraReport rep;
   const std::vector<LoraModule> mods = load_lora_modules(unet_weight_specs(u.config()), st, strength, &rep);
-  for (const LoraModule& m : mods) {
-    void* dev = nullptr;
-    const size_t na = m.a_fp16.size(), nb = m.b_fp16.size();
-    DLM_CALL(dlm_malloc(&dev, (na + nb) * 2));
-    std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
-    DLM_CALL(dlm_memcpy(dev, m.a_fp16.data(), na * 2, 0));
-    DLM_CALL(dlm_memcpy(static_cast<uint16_t*>(dev) + na, m.b_fp16.data(), nb * 2, 0));
-    u.apply_lora(m.base_key, dev, static_cast<uint16_t*>(dev) + na, m.rank, m.in_flat, m.out_dim, m.scale,
-                 stream);
-  }
+  for (const LoraModule& m : mods) unet_apply_lora_module(u, m, stream);
   if (report) *report = rep;
+}
+
+void unet_apply_lora_module(UNet& u, const LoraModule& m, void* stream) {
+  const size_t na = m.a_fp16.size(), nb = m.b_fp16.size();
+  if (m.rank <= 0 || na != (size_t)m.rank * m.in_flat || nb != (size_t)m.out_dim * m.rank)
+    throw std::runtime_error("lora: module '" + m.base_key + "' has inconsistent A / B sizes");
+  void* dev = nullptr;
+  DLM_CALL(dlm_malloc(&dev, (na + nb) * 2));
+  std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
+  DLM_CALL(dlm_memcpy(dev, m.a_fp16.data(), na * 2, 0));
+  DLM_CALL(dlm_memcpy(static_cast<uint16_t*>(dev) + na, m.b_fp16.data(), nb * 2, 0));
+  u.apply_lora(m.base_key, dev, static_cast<uint16_t*>(dev) + na, m.rank, m.in_flat, m.out_dim, m.scale,
+               stream);
 }
 
 }  // namespace dollama

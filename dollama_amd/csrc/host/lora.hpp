@@ -49,5 +49,7 @@ uint16_t f32_to_f16_rne(float v);
 // Modules applied before a failing one stay applied.
 void unet_apply_lora_file(UNet& u, const std::string& path, float strength, LoraReport* report,
                           void* stream);
+// Merge one resolved module (W += scale * (B @ A)) into the resident weights.
+void unet_apply_lora_module(UNet& u, const LoraModule& m, void* stream);
 
 }  // namespace dollama

@@ -105,26 +105,25 @@ void denoise(UNet& unet, const DenoiseArgs& a, void* stream, bool cfg) {
 
 namespace {
 template <class Net>
-void load_safetensors(Net& net, const std::vector<WeightSpec>& specs, const std::string& path,
-                      void* stream) {
-  SafeTensors st(path);
+void load_safetensors(Net& net, const std::vector<WeightSpec>& specs, const SafeTensors& st,
+                      const std::string& what, void* stream) {
   // one upload of the whole data region, tensors registered in place
   void* dev = nullptr;
   DLM_CALL(dlm_malloc(&dev, st.data_bytes()));
   std::unique_ptr<void, void (*)(void*)> hold(dev, [](void* p) { (void)dlm_free(p); });
   DLM_CALL(dlm_memcpy(dev, st.data(), st.data_bytes(), 0));
   for (const WeightSpec& s : specs) {
-    if (!st.has(s.name)) throw std::runtime_error("safetensors: missing '" + s.name + "' in " + path);
+    if (!st.contains(s.name)) throw std::runtime_error("safetensors: missing '" + s.name + "' in " + what);
     if (st.dtype(s.name) != StDtype::F16)
       throw std::runtime_error("safetensors: '" + s.name + "' is not F16");
     if (st.offset(s.name) % 2 != 0) throw std::runtime_error("safetensors: misaligned tensor");
-    net.set_weight(s.name, static_cast<char*>(dev) + st.offset(s.name), st.shape(s.name));
+    net.set_weight(s.name, static_cast<char*>(dev) + st.offset(s.name), st.shape_i64(s.name));
   }
   net.prepare(stream);  // packs into the handle's memory and synchronises
 }
 
 std::vector<uint16_t> f16_tensor(const SafeTensors& st, const std::string& name, size_t expect) {
-  if (!st.has(name)) throw std::runtime_error("embeds: missing '" + name + "'");
+  if (!st.contains(name)) throw std::runtime_error("embeds: missing '" + name + "'");
   if (st.dtype(name) != StDtype::F16) throw std::runtime_error("embeds: '" + name + "' is not F16");
   size_t nbytes = 0;
   const uint8_t* p = st.tensor_bytes(name, nbytes);
@@ -149,11 +148,17 @@ std::vector<uint16_t> to_f16(const float* x, size_t n) {
 }  // namespace
 
 void load_unet_safetensors(UNet& u, const std::string& path, void* stream) {
-  load_safetensors(u, unet_weight_specs(u.config()), path, stream);
+  const SafeTensors st(path);
+  load_safetensors(u, unet_weight_specs(u.config()), st, path, stream);
+}
+
+void load_unet_safetensors(UNet& u, const SafeTensors& st, void* stream) {
+  load_safetensors(u, unet_weight_specs(u.config()), st, "the safetensors file", stream);
 }
 
 void load_vae_safetensors(VAE& v, const std::string& path, void* stream) {
-  load_safetensors(v, vae_weight_specs(v.config()), path, stream);
+  const SafeTensors st(path);
+  load_safetensors(v, vae_weight_specs(v.config()), st, path, stream);
 }
 
 // ------------------------------------------------------------------ pipeline

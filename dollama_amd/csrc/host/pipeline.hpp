@@ -19,6 +19,7 @@
 #include <string>
 #include <vector>
 
+#include "safetensors.hpp"
 #include "unet.hpp"
 #include "vae.hpp"
 
@@ -78,6 +79,7 @@ void denoise(UNet& unet, const DenoiseArgs& a, void* stream, bool cfg = true);
 // Load every tensor the network reads from a diffusers-named fp16
 // safetensors file and prepare the handle.
 void load_unet_safetensors(UNet& u, const std::string& path, void* stream);
+void load_unet_safetensors(UNet& u, const SafeTensors& st, void* stream);
 void load_vae_safetensors(VAE& v, const std::string& path, void* stream);
 
 // Reference DiffusionPipeline (src/infer/diffusion.cuh:62-178) over the

@@ -46,7 +46,7 @@ float f16_to_f32(uint16_t h) {
 }
 
 std::vector<float> f32_of(const SafeTensors& st, const std::string& name, size_t expect) {
-  if (!st.has(name)) throw std::runtime_error("embeds: missing '" + name + "'");
+  if (!st.contains(name)) throw std::runtime_error("embeds: missing '" + name + "'");
   if (st.dtype(name) != StDtype::F16) throw std::runtime_error("embeds: '" + name + "' is not F16");
   size_t nbytes = 0;
   const uint8_t* p = st.tensor_bytes(name, nbytes);
@@ -74,10 +74,10 @@ class SdxlBackend : public IDiffusionBackend {
     cond_ehs_ = f32_of(st, "input_encoder_hidden_states_f16", ne);
     cond_txt_ = f32_of(st, "input_text_embeds_f16", nt);
     ids_ = f32_of(st, "input_time_ids_f16", 6);
-    uncond_ehs_ = st.has("uncond_encoder_hidden_states_f16")
+    uncond_ehs_ = st.contains("uncond_encoder_hidden_states_f16")
                       ? f32_of(st, "uncond_encoder_hidden_states_f16", ne)
                       : std::vector<float>(ne, 0.0f);
-    uncond_txt_ = st.has("uncond_text_embeds_f16") ? f32_of(st, "uncond_text_embeds_f16", nt)
+    uncond_txt_ = st.contains("uncond_text_embeds_f16") ? f32_of(st, "uncond_text_embeds_f16", nt)
                                                    : std::vector<float>(nt, 0.0f);
   }
 

@@ -1,6 +1,8 @@
 // safetensors reader (see safetensors.hpp).
 #include "safetensors.hpp"
 
+#include <algorithm>
+
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -182,6 +184,10 @@ void SafeTensors::parse_header(const std::string& json) {
   Json j(json);
   j.expect('{');
   if (j.peek('}')) return;
+  struct SortNames {  // names() lists tensors in dictionary order on return
+    std::vector<std::string>& v;
+    ~SortNames() { std::sort(v.begin(), v.end()); }
+  } sort_names{names_};
   while (true) {
     const std::string key = j.str();
     j.expect(':');
@@ -217,6 +223,7 @@ void SafeTensors::parse_header(const std::string& json) {
         if (d < 0) j.fail("negative dimension");
         if (__builtin_mul_overflow(n, (size_t)d, &n))
           throw std::runtime_error("safetensors: tensor '" + key + "' shape overflows");
+        e.shape_u.push_back((size_t)d);
       }
       const size_t es = dtype_size(e.dtype);
       size_t nbytes = 0;
@@ -224,6 +231,7 @@ void SafeTensors::parse_header(const std::string& json) {
         throw std::runtime_error("safetensors: tensor '" + key + "' byte size overflows");
       if (es != 0 && nbytes != e.end - e.begin)
         throw std::runtime_error("safetensors: tensor '" + key + "' size does not match shape");
+      if (entries_.count(key)) j.fail("duplicate tensor name");
       entries_[key] = e;
       names_.push_back(key);
     }
@@ -243,7 +251,8 @@ const SafeTensors::Entry& SafeTensors::entry(const std::string& name) const {
 }
 
 StDtype SafeTensors::dtype(const std::string& name) const { return entry(name).dtype; }
-const std::vector<int64_t>& SafeTensors::shape(const std::string& name) const { return entry(name).shape; }
+const std::vector<size_t>& SafeTensors::shape(const std::string& name) const { return entry(name).shape_u; }
+const std::vector<int64_t>& SafeTensors::shape_i64(const std::string& name) const { return entry(name).shape; }
 size_t SafeTensors::offset(const std::string& name) const { return entry(name).begin; }
 
 const uint8_t* SafeTensors::tensor_bytes(const std::string& name, size_t& nbytes) const {

@@ -1,7 +1,9 @@
 // Read-only safetensors file (memory-mapped) with a minimal header parser.
 //
-// Keeps the reference loader's surface (src/io/safetensors.hpp:108):
-// names(), dtype(name), shape(name), tensor_bytes(name, nbytes).  Format:
+// Keeps the reference loader's surface (src/io/safetensors.hpp:108-150):
+// names() in dictionary order, contains(name), dtype(name), shape(name) as
+// std::vector<size_t>, tensor_bytes(name, nbytes); an unknown name throws
+// std::runtime_error.  Format:
 // 8-byte little-endian header length, a JSON object mapping each tensor name
 // to {"dtype", "shape", "data_offsets": [begin, end]} (offsets relative to
 // the end of the header), optional "__metadata__", then the raw data.
@@ -25,9 +27,11 @@ class SafeTensors {
   SafeTensors& operator=(const SafeTensors&) = delete;
 
   const std::vector<std::string>& names() const { return names_; }
-  bool has(const std::string& name) const { return entries_.count(name) != 0; }
+  bool contains(const std::string& name) const { return entries_.count(name) != 0; }
   StDtype dtype(const std::string& name) const;
-  const std::vector<int64_t>& shape(const std::string& name) const;
+  const std::vector<size_t>& shape(const std::string& name) const;
+  // the same shape as signed extents (the UNet / VAE weight specs' type)
+  const std::vector<int64_t>& shape_i64(const std::string& name) const;
   const uint8_t* tensor_bytes(const std::string& name, size_t& nbytes) const;
   // whole data region (for a single upload)
   const uint8_t* data() const { return data_; }
@@ -38,6 +42,7 @@ class SafeTensors {
   struct Entry {
     StDtype dtype = StDtype::Unknown;
     std::vector<int64_t> shape;
+    std::vector<size_t> shape_u;
     size_t begin = 0, end = 0;
   };
   const Entry& entry(const std::string& name) const;

@@ -57,13 +57,43 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line) {
 // and share that stream's slots; another stream gets its own, so calls on two
 // streams never race on one buffer.  Growth synchronises the device before
 // freeing the old block, so stream-ordered users never see it vanish.
+// Bounded: when a request would take the device's total above
+// kScratchDeviceCap, the device is synchronised and every slot of the other
+// streams on it is freed first (they are re-created on their next use), so a
+// caller that cycles through many streams does not accumulate a set per
+// stream.  dlm_scratch_release(stream) frees one stream's slots explicitly
+// (for a stream about to be destroyed: its handle may be reused by a new
+// stream).
 namespace {
 struct ScratchSlot {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
+constexpr size_t kScratchDeviceCap = size_t(2) << 30;
 std::mutex g_scratch_mu;
 std::map<std::tuple<int, hipStream_t, int>, ScratchSlot> g_scratch;
+
+size_t device_total(int dev) {
+  size_t t = 0;
+  for (const auto& kv : g_scratch)
+    if (std::get<0>(kv.first) == dev) t += kv.second.bytes;
+  return t;
+}
+
+// frees the slots of `dev` whose stream is not `keep`; the caller holds the
+// lock and has synchronised the device
+bool evict_other_streams(int dev, hipStream_t keep) {
+  bool ok = true;
+  for (auto it = g_scratch.begin(); it != g_scratch.end();) {
+    if (std::get<0>(it->first) == dev && std::get<1>(it->first) != keep) {
+      if (it->second.ptr && hipFree(it->second.ptr) != hipSuccess) ok = false;
+      it = g_scratch.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return ok;
+}
 }  // namespace
 
 void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status) {
@@ -76,23 +106,59 @@ void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   ScratchSlot& s = g_scratch[{dev, stream, slot}];
   if (s.bytes >= bytes && s.ptr) return s.ptr;
+  size_t want = bytes < 256 ? 256 : bytes;
+  want = (want + 0xFFFFF) & ~size_t(0xFFFFF);  // round to 1 MiB
+  const bool over = device_total(dev) - s.bytes + want > kScratchDeviceCap;
+  if (s.ptr || over) {
+    if (hipDeviceSynchronize() != hipSuccess) {
+      *status = fail(DLM_ERR_HIP, "scratch: device synchronisation failed");
+      return nullptr;
+    }
+  }
   if (s.ptr) {
-    if (hipDeviceSynchronize() != hipSuccess || hipFree(s.ptr) != hipSuccess) {
+    if (hipFree(s.ptr) != hipSuccess) {
       *status = fail(DLM_ERR_HIP, "scratch: release of old block failed");
       return nullptr;
     }
     s.ptr = nullptr;
     s.bytes = 0;
   }
-  size_t want = bytes < 256 ? 256 : bytes;
-  want = (want + 0xFFFFF) & ~size_t(0xFFFFF);  // round to 1 MiB
-  if (hipMalloc(&s.ptr, want) != hipSuccess) {
-    s.ptr = nullptr;
+  if (over && !evict_other_streams(dev, stream)) {
+    *status = fail(DLM_ERR_HIP, "scratch: release of other streams' blocks failed");
+    return nullptr;
+  }
+  ScratchSlot& t = g_scratch[{dev, stream, slot}];  // eviction never erases this stream's slots
+  if (hipMalloc(&t.ptr, want) != hipSuccess) {
+    t.ptr = nullptr;
     *status = fail(DLM_ERR_OUT_OF_MEMORY, "scratch: hipMalloc of " + std::to_string(want) + " bytes failed");
     return nullptr;
   }
-  s.bytes = want;
-  return s.ptr;
+  t.bytes = want;
+  return t.ptr;
+}
+
+int scratch_release(hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  bool any = false;
+  for (const auto& kv : g_scratch) any |= std::get<1>(kv.first) == stream;
+  if (!any) return DLM_OK;
+  if (hipStreamSynchronize(stream) != hipSuccess) return fail(DLM_ERR_HIP, "scratch: stream synchronisation failed");
+  for (auto it = g_scratch.begin(); it != g_scratch.end();) {
+    if (std::get<1>(it->first) == stream) {
+      if (it->second.ptr && hipFree(it->second.ptr) != hipSuccess) return fail(DLM_ERR_HIP, "scratch: hipFree failed");
+      it = g_scratch.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return DLM_OK;
+}
+
+size_t scratch_bytes() {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  size_t t = 0;
+  for (const auto& kv : g_scratch) t += kv.second.bytes;
+  return t;
 }
 
 }  // namespace dlm
@@ -100,6 +166,18 @@ void* scratch_slot(size_t bytes, int slot, hipStream_t stream, int* status) {
 extern "C" {
 
 const char* dlm_last_error(void) { return dlm::g_last_error.c_str(); }
+
+int dlm_scratch_release(void* stream) {
+  const int st = dlm::scratch_release((hipStream_t)stream);
+  if (st != DLM_OK) return st;
+  return dlm::split_workspace_release((hipStream_t)stream);
+}
+
+int dlm_scratch_bytes(size_t* bytes) {
+  DLM_REQUIRE(bytes != nullptr, "bytes is NULL");
+  *bytes = dlm::scratch_bytes() + dlm::split_workspace_bytes();
+  return DLM_OK;
+}
 
 void dlm_set_last_error(const char* msg) { dlm::g_last_error = msg ? msg : ""; }
 

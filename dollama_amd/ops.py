@@ -590,3 +590,37 @@ def sdxl_embed_inputs(timesteps: torch.Tensor, text_embeds: torch.Tensor, time_i
     call("dlm_sdxl_embed_inputs_fp16", _p(timesteps), _p(text_embeds), 1280, _p(time_ids), stride,
          256, _p(t_emb), 320, _p(add_in), B, stream_handle())
     return t_emb, add_in
+
+
+def euler_cfg_step(latent: torch.Tensor, noise: torch.Tensor, model_in: torch.Tensor, guidance: float,
+                   sigma: float, sigma_next: float, in_scale: float):
+    """In place: latent (fp32 [n]) += (u + g (c - u)) * (sigma_next - sigma)
+    with noise fp16 [2, n] (cond first); model_in fp16 [2, n] receives
+    fp16(latent * in_scale) twice (reference src/infer/diffusion.cu:968-973,
+    src/infer/scheduler.hpp:112-143)."""
+    n = latent.numel()
+    _need(latent, n, "latent", dtype=torch.float32)
+    _need(noise, 2 * n, "noise")
+    _need(model_in, 2 * n, "model_in")
+    call("dlm_euler_cfg_step", _p(latent), _p(noise), _p(model_in), n, float(guidance), float(sigma),
+         float(sigma_next), float(in_scale), stream_handle())
+
+
+def euler_step(latent: torch.Tensor, noise: torch.Tensor, model_in: torch.Tensor, sigma: float,
+               sigma_next: float, in_scale: float):
+    """In place: latent += noise * (sigma_next - sigma), model_in =
+    fp16(latent * in_scale) (one prediction, no guidance)."""
+    n = latent.numel()
+    _need(latent, n, "latent", dtype=torch.float32)
+    _need(noise, n, "noise")
+    _need(model_in, n, "model_in")
+    call("dlm_euler_step", _p(latent), _p(noise), _p(model_in), n, float(sigma), float(sigma_next),
+         float(in_scale), stream_handle())
+
+
+def scale_latent(latent: torch.Tensor, model_in: torch.Tensor, scale: float, copies: int):
+    """model_in[c, :] = fp16(latent * scale) for c < copies."""
+    n = latent.numel()
+    _need(latent, n, "latent", dtype=torch.float32)
+    _need(model_in, copies * n, "model_in")
+    call("dlm_scale_latent_fp16", _p(latent), _p(model_in), n, float(scale), int(copies), stream_handle())

@@ -89,6 +89,19 @@ int dlm_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* s
 int dlm_memset_async(void* dst, int value, size_t bytes, void* stream);
 int dlm_device_synchronize(void);
 int dlm_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+/* Library staging of the reference-layout entry points (dlm_conv2d_fp16,
+ * dlm_gemm_fp16, dlm_attention_fp16) and the split-K workspace of the
+ * channels-last GEMMs are kept per (device, stream) and grow on first use;
+ * staging of other streams is dropped when a device's total would pass
+ * 2 GiB.  dlm_scratch_release synchronises `stream` and frees everything
+ * the library holds for it: call it before destroying a stream that ran
+ * library entry points (a new stream may reuse the handle).  Graphs captured
+ * on that stream must not be replayed afterwards.  No reference counterpart
+ * (the reference's launch_* wrappers cudaMalloc / cudaFree per call).
+ * dlm_scratch_bytes reports the device bytes the library holds for all
+ * streams. */
+int dlm_scratch_release(void* stream);
+int dlm_scratch_bytes(size_t* bytes);
 
 int dlm_stream_create(void** stream);
 int dlm_stream_destroy(void* stream);
@@ -118,7 +131,9 @@ int dlm_event_elapsed_ms(float* ms, void* start, void* stop);
  * Replaces dollama::launch_conv2d (src/kernels/conv2d.cuh:38-40).  Stages the
  * input channels-last and the packed weight in library buffers kept per
  * (device, stream); they grow on first use (hipMalloc after a device
- * synchronisation), so warm the call before capturing it into a graph. */
+ * synchronisation).  Not for graph capture: a later call may re-allocate
+ * the staging a captured launch reads (dlm_conv2d_fp16_noalloc is the
+ * capturable form). */
 int dlm_conv2d_fp16(const void* in, const void* weight, const void* bias, void* out,
                     int N, int Cin, int H, int W, int Cout, int KH, int KW,
                     int stride_h, int stride_w, int pad_h, int pad_w,
@@ -143,7 +158,10 @@ int dlm_conv2d_fp16_noalloc(const void* in, const void* weight, const void* bias
                             int dilation_h, int dilation_w, void* stream);
 
 /* C = alpha * op(A) op(B) + beta * C, row-major, fp16 in/out, fp32 accumulate.
- * op(A) = [M,K], op(B) = [K,N].
+ * op(A) = [M,K], op(B) = [K,N].  Operands that are not [M,K] / [N,K] with
+ * 16-byte aligned rows are first copied (transposed, K padded to a multiple
+ * of 8) into per-stream library staging, so like dlm_conv2d_fp16 this entry
+ * is not for graph capture.
  * Replaces dollama::launch_gemm_fp16 (src/kernels/gemm.cuh:44-53). */
 int dlm_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K,
                   float alpha, float beta, int transA, int transB, void* stream);
@@ -160,9 +178,13 @@ int dlm_group_norm_fp16(const void* in, const void* gamma, const void* beta, voi
 int dlm_layer_norm_fp16(const void* in, const void* gamma, const void* beta, void* out,
                         int rows, int C, float eps, void* stream);
 
-/* O = softmax(scale * Q K^T) V, Q/O [B,H,Sq,Dh], K/V [B,H,Sk,Dh], fp32 softmax.
- * Dh must be 64.  Replaces launch_attention / launch_attention_fast
- * (src/kernels/attention.cuh:53-73). */
+/* O = softmax(scale * Q K^T) V, Q/O [B,H,Sq,Dh], K/V [B,H,Sk,Dh], fp32 softmax,
+ * any head size (as launch_attention picks a path by Dh,
+ * src/kernels/attention.cu:18-21): Dh = 64 runs the flash kernel over a
+ * transposed-V copy, other head sizes an fp32 scores GEMM, a row softmax and
+ * a P V^T GEMM in row chunks whose scores stay within 256 MiB.  The copies
+ * live in per-stream library staging: not for graph capture.  Replaces
+ * launch_attention / launch_attention_fast (src/kernels/attention.cuh:53-73). */
 int dlm_attention_fp16(const void* q, const void* k, const void* v, void* out,
                        int B, int H, int Sq, int Sk, int Dh, float scale, void* stream);
 
@@ -192,36 +214,6 @@ int dlm_conv_bias_residual_fp16(const void* conv, const void* convbias, const vo
  * Replaces launch_timestep_embedding (src/kernels/timeembed.cuh:44-47). */
 int dlm_timestep_embedding_fp16(void* out, float timestep, int dim, float max_period,
                                 void* stream);
-
-/* Tuning aids: force the MFMA GEMM / conv tile configuration, and the
- * split-K factor, for every following launch in this process (0 =
- * automatic).  Tiles 1-7: the register-staged core (128x128, 128x64, 64x64,
- * 128x32, 256x128, 128x256, 256x256); 8-25: the LDS-DMA core
- * (BMxBN, wave tile, ring depth) = 8 128x128 64x64 2, 9 128x64 64x32 2,
- * 10 128x128 64x64 4, 11 128x64 64x32 4, 12 64x128 32x64 2,
- * 13 256x128 128x64 2, 14 128x128 64x32 4, 15 128x128 64x32 2,
- * 16 256x128 64x64 2, 17 128x128 32x64 4, 18 128x128 64x32 5,
- * 19 256x128 64x64 3, 20 128x64 64x32 6, 21 256x160 64x80 3,
- * 22 128x160 32x80 3, 23 128x160 64x80 2, 24 128x160 32x80 4,
- * 25 64x160 32x80 2, 26 128x80 16x80 5; 27-34 the same core with the next
- * slice's first fragments read during the current slice's last MFMAs:
- * 27 128x80 16x80 5, 28 256x160 64x80 3, 29 128x128 64x32 2,
- * 30 128x160 32x80 4, 31 128x160 32x80 3, 32 256x128 64x64 3,
- * 33 128x128 64x32 4, 34 128x64 64x32 2; 35-39 ring stages of two K
- * slices under one barrier (BMxBN, wave tile, stages): 35 128x80 16x80 3,
- * 36 128x80 16x80 2, 37 128x160 32x80 2, 38 128x128 64x32 2,
- * 39 128x64 64x32 3.  Splits apply to the LDS-DMA core only. */
-int dlm_gemm_force_tile(int tile_id);
-/* Same override for GEMMs / convs of one shape (M, N = output columns,
- * K = reduction length); tile 0 and splits 0 remove it, M = N = K = 0 clears
- * every override.  Like every tuning aid here it is thread-local: it steers
- * only launches made by the calling thread. */
-int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits);
-int dlm_gemm_force_split(int splits);
-/* Tuning aid: select alternative tile heuristics (0 = default; bit 0 = no
- * 160-column / split-K rules; bit 1 = no fragment-prefetch forms, four
- * splits for 256x160 grids that fill the chip). */
-int dlm_gemm_set_variant(int variant);
 
 /* ------------------------------------------------------------------ */
 /* Channels-last fused entry points (native forms used by the UNet)     */
@@ -290,7 +282,8 @@ int dlm_linear_vt_ln_fp16(const void* X, int lda, const void* W, int ldw, const 
                           int tokens, int vt_ld, int M, int N, int K, void* stream);
 /* Weight side of the fold: W_out[n] = fp16(W[n] * gamma) (a copy when gamma
  * is NULL), c1[n] = sum_k W_out[n][k], c2[n] = sum_k lnbeta[k] W[n][k] + b[n]
- * (fp32; lnbeta / b may be NULL).  W_out may alias W. */
+ * (fp32; lnbeta / b may be NULL).  W_out may be W itself (in place, with
+ * ldo == ldw); any other overlap of the two is DLM_ERR_INVALID_ARG. */
 int dlm_ln_fold_fp16(const void* W, int ldw, int N, int K, const void* gamma, const void* lnbeta,
                      const void* b, void* W_out, int ldo, float* c1, float* c2, void* stream);
 

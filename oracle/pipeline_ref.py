@@ -9,6 +9,11 @@ guidance a B=1 UNet on the cond embeddings and eps = its prediction
 (:551-700); then latent / scaling_factor -> VAE decode -> RGB8 (:980-998,
 image_f16_to_rgb_u8 :146-165).  Everything in fp32 (no fp16 rounding of
 the model input, the conditioning or the image).
+
+The per-step pieces (scale_model_input, cfg_combine, euler_step) are
+separate functions so the tests can pin each one: the first and last
+against the reference's own scheduler header compiled on the CPU, the CFG
+combine and its slot order against a stub noise predictor.
 """
 from __future__ import annotations
 
@@ -22,6 +27,41 @@ from . import unet_ref as OR
 from . import vae_ref as OV
 
 
+def scale_model_input(sample, sigma):
+    """sample / sqrt(sigma^2 + 1) (src/infer/scheduler.hpp:112-120)."""
+    return sample / math.sqrt(float(sigma) ** 2 + 1.0)
+
+
+def cfg_combine(noise, guidance):
+    """Classifier-free guidance over a batch-2 prediction whose slot 0 ran on
+    the cond embeddings and slot 1 on the uncond ones (the reference copies
+    cond into the first half of d_ehs2 / d_txt2 and uncond into the second,
+    diffusion.cu:878-883, and reads d_noise2 back the same way, :928-931):
+    u + g (c - u) (:968-973)."""
+    c, u = noise[0:1], noise[1:2]
+    return u + guidance * (c - u)
+
+
+def euler_step(sample, eps, sigma, sigma_next):
+    """Euler step with an epsilon prediction: sample + eps * (sigma_next -
+    sigma) (src/infer/scheduler.hpp:122-143)."""
+    return sample + eps * (float(sigma_next) - float(sigma))
+
+
+def denoise(unet_fn, sig, ts, lat, ehs, txt, ids, *, guidance=7.5, cfg=True):
+    """The sampling loop on an fp32 latent [1, C, h, w]; unet_fn(x, t, ehs,
+    txt, ids) returns the noise prediction for a batch (B = 2 with cond then
+    uncond rows when cfg, else 1).  Returns the final latent."""
+    B = 2 if cfg else 1
+    for i in range(len(ts)):
+        x = scale_model_input(lat, sig[i])
+        t = torch.full((B,), float(ts[i]))
+        out = unet_fn(x.expand(B, -1, -1, -1).contiguous(), t, ehs, txt, ids)
+        eps = cfg_combine(out, guidance) if cfg else out
+        lat = euler_step(lat, eps, sig[i], sig[i + 1])
+    return lat
+
+
 def txt2img(unet_w, ucfg, vae_w, vcfg, *, seed, steps, lh, lw, cond_ehs, cond_text, time_ids,
             uncond_ehs=None, uncond_text=None, guidance=7.5, cfg=True, scaling_factor=0.13025):
     """RGB8 [1, 8 lh, 8 lw, 3] (torch uint8) and the final latent."""
@@ -33,13 +73,11 @@ def txt2img(unet_w, ucfg, vae_w, vcfg, *, seed, steps, lh, lw, cond_ehs, cond_te
     if cfg:
         ehs = torch.cat([ehs, uncond_ehs.reshape(1, -1, ucfg.cross_dim).float()], 0)
         txt = torch.cat([txt, uncond_text.reshape(1, -1).float()], 0)
-    B = 2 if cfg else 1
     ids = time_ids.reshape(6).float()
-    for i in range(steps):
-        x = lat / math.sqrt(float(sig[i]) ** 2 + 1.0)
-        t = torch.full((B,), float(ts[i]))
-        out = OR.unet_forward(unet_w, ucfg, x.expand(B, -1, -1, -1).contiguous(), t, ehs, txt, ids)
-        eps = out[1:2] + guidance * (out[0:1] - out[1:2]) if cfg else out
-        lat = lat + eps * (float(sig[i + 1]) - float(sig[i]))
+
+    def unet_fn(x, t, e, tx, i):
+        return OR.unet_forward(unet_w, ucfg, x, t, e, tx, i)
+
+    lat = denoise(unet_fn, sig, ts, lat, ehs, txt, ids, guidance=guidance, cfg=cfg)
     img = OV.vae_decode(vae_w, vcfg, lat / scaling_factor)
     return OV.image_to_rgb8(img), lat

@@ -61,6 +61,14 @@ def test_noalloc_conv_matches_allocating_entry_point(gpu):
     x, w, b, y_ref, y_na = _case(gpu, (2, 64, 17, 23, 96, 3, 3), (1, 2, 2, 1, 2, 2), 50)
     assert torch.equal(y_na, y_ref), "noalloc conv differs from dlm_conv2d_fp16 (call 2)"
     assert_close(y_na, R.conv2d(x, w, b, (1, 2), (2, 1), (2, 2)), "noalloc conv call 2 vs oracle")
+    # the strided / dilated call allocates nothing either
+    xg, wg, bg = to_gpu(x), to_gpu(w), to_gpu(b)
+    torch.cuda.synchronize()
+    before = torch.cuda.mem_get_info()[0]
+    assert _conv("dlm_conv2d_fp16_noalloc", xg, wg, bg, y_na, (1, 2, 2, 1, 2, 2)) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == before
+    assert torch.equal(y_na, y_ref)
     # a third call, again of the first shape, after the smaller one
     x, w, b, y_ref, y_na = _case(gpu, (1, 320, 128, 128, 320, 3, 3), (1, 1, 1, 1, 1, 1), 60)
     assert torch.equal(y_na, y_ref), "noalloc conv differs from dlm_conv2d_fp16 (call 3)"
@@ -73,6 +81,41 @@ def test_noalloc_conv_matches_allocating_entry_point(gpu):
     torch.cuda.synchronize()
     assert torch.cuda.mem_get_info()[0] == before
     assert torch.equal(y_na, y_ref)
+
+
+def test_noalloc_conv_under_graph_capture(gpu):
+    """Captured into a HIP graph (the callers it is for), the conv replays
+    bit-identical to its eager call, also after eager calls of another shape
+    have overwritten the shared staging array between replays."""
+    print("[case] noalloc conv captured: 2x320x64x64 -> 320 3x3, replays between eager calls",
+          flush=True)
+    x = to_gpu(randn((2, 320, 64, 64), 70))
+    w = to_gpu(randn((320, 320, 3, 3), 71, std=0.02))
+    b = to_gpu(randn((320,), 72, std=0.01))
+    geom = (1, 1, 1, 1, 1, 1)
+    y_eager = torch.empty(2, 320, 64, 64, dtype=torch.float16, device=gpu)
+    y_graph = torch.full_like(y_eager, float("nan"))
+    assert _conv("dlm_conv2d_fp16_noalloc", x, w, b, y_eager, geom) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    # another shape, run eagerly between replays to clobber the staging array
+    xo = to_gpu(randn((2, 64, 17, 23), 73))
+    wo = to_gpu(randn((96, 64, 3, 3), 74, std=0.02))
+    bo = to_gpu(randn((96,), 75, std=0.01))
+    yo = torch.empty(2, 96, 17, 23, dtype=torch.float16, device=gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        assert _conv("dlm_conv2d_fp16_noalloc", x, w, b, y_graph, geom) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y_graph.fill_(float("nan"))
+        assert _conv("dlm_conv2d_fp16_noalloc", xo, wo, bo, yo, geom) == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_eager), f"graph replay {rep} differs from the eager call"
+    del graph
 
 
 def test_noalloc_conv_rejects_staging_beyond_the_fixed_maximum(gpu):
