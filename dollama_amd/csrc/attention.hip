@@ -305,7 +305,8 @@ __device__ __forceinline__ float fa_sum_halves(float x) {
 // would otherwise leave SIMDs with a single wave).  Each wave issues 8 / NWV
 // of the 8-row DMA groups of every K and V^T tile.
 template <int NWV>
-__global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p) {
+__global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2)))
+flash_vt_pipe_kernel(FlashVtParams p) {
   constexpr int DI = 8 / NWV;  // DMA instructions per wave per operand tile
   __shared__ __attribute__((aligned(1024))) unsigned char smem_g[FA_NS * FA_STAGE];
   unsigned char DLM_LDS* smem = (unsigned char DLM_LDS*)smem_g;
@@ -329,13 +330,19 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   const int g = lane >> 5;
   const int q0 = qb * (NWV * 32) + wave * 32;
 
+  // Q scaled by c = scale * log2(e) once (one fp16 rounding of q * c), so the
+  // scores come out of the MFMA in the exponent's units
   f16x8 qf[4];
   {
     const int qi = q0 + (lane & 31);
     const f16* qp = p.q + b * p.q_sb + h * p.q_sh + (long long)qi * p.q_ss + g * 8;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-      qf[ds] = qi < p.Sq ? *reinterpret_cast<const f16x8*>(qp + ds * 16) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int ds = 0; ds < 4; ++ds) {
+      f16x8 v = qi < p.Sq ? *reinterpret_cast<const f16x8*>(qp + ds * 16) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = (f16)((float)v[t] * p.c);
+      qf[ds] = v;
+    }
   }
 
   const i32x4 rk = fa_rsrc(p.k, p.k_bytes);
@@ -357,15 +364,22 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
   auto issue = [&](int buf, int kt) {
     unsigned char DLM_LDS* st = smem + buf * FA_STAGE;
     const int k0 = kt * FA_TK;
-    const bool part = k0 + FA_TK > p.Sk;
+    if (k0 + FA_TK <= p.Sk) {  // a full tile (all but a partial last one): no masking
+#pragma unroll
+      for (int i = 0; i < DI; ++i) fa_dma16(rk, st + (wave * DI + i) * 1024, koff[i] + kt * kstep);
+#pragma unroll
+      for (int i = 0; i < DI; ++i)
+        fa_dma16(rv, st + FA_TILE + (wave * DI + i) * 1024, voff[i] + kt * (FA_TK * 2));
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < DI; ++i) {
-      const bool in = !part || k0 + fa_perm(dma_row(i)) < p.Sk;
+      const bool in = k0 + fa_perm(dma_row(i)) < p.Sk;
       fa_dma16(rk, st + (wave * DI + i) * 1024, in ? koff[i] + kt * kstep : kFaOOB);
     }
 #pragma unroll
     for (int i = 0; i < DI; ++i) {
-      const bool in = !part || k0 + dma_chunk(dma_row(i)) * 8 < p.Sk;
+      const bool in = k0 + dma_chunk(dma_row(i)) * 8 < p.Sk;
       fa_dma16(rv, st + FA_TILE + (wave * DI + i) * 1024, in ? voff[i] + kt * (FA_TK * 2) : kFaOOB);
     }
   };
@@ -373,25 +387,39 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     const int c = chunk ^ ((row >> 1) & 7);
     return *reinterpret_cast<const f16x8 DLM_LDS*>(st + row * 128 + c * 16);
   };
-  // S^T = K Q^T of the tile in st: lane = query, element e of block kb = LDS
-  // key row kb*32 + 8*(e>>2) + 4g + (e&3)
-  auto scores = [&](const unsigned char DLM_LDS* st, f32x16 (&sv)[2]) {
+  // S^T = init + K (c Q)^T of the tile in st: lane = query, element e of
+  // block kb = LDS key row kb*32 + 8*(e>>2) + 4g + (e&3).  init is the
+  // accumulator's start: -m (the lane's running max, broadcast), so the
+  // scores leave the MFMA already shifted and p = 2^s needs no VALU
+  // subtraction.
+  // The two key blocks' chains alternate, so consecutive MFMAs are
+  // independent and VALU work can issue between dependent ones.
+  auto scores = [&](const unsigned char DLM_LDS* st, f32x16 (&sv)[2], const f32x16& init) {
+    f16x8 kf[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f16x8 kf[4];
+    for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) kf[ds] = frag(st, kb * 32 + (lane & 31), 2 * ds + g);
-      sv[kb] = mfma32x32x16(kf[0], qf[0], f32x16{});
+      for (int kb = 0; kb < 2; ++kb) kf[kb][ds] = frag(st, kb * 32 + (lane & 31), 2 * ds + g);
 #pragma unroll
-      for (int ds = 1; ds < 4; ++ds) sv[kb] = mfma32x32x16(kf[ds], qf[ds], sv[kb]);
-    }
+    for (int kb = 0; kb < 2; ++kb) sv[kb] = mfma32x32x16(kf[kb][0], qf[0], init);
+#pragma unroll
+    for (int ds = 1; ds < 4; ++ds)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sv[kb] = mfma32x32x16(kf[kb][ds], qf[ds], sv[kb]);
   };
 
   const int nkt = (p.Sk + FA_TK - 1) / FA_TK;
   issue(0, 0);
   if (nkt > 1) issue(1, 1);
 
-  float m_run = -INFINITY, l_run = 0.0f;
+  // Running state, in log2 units: the scores of a tile arrive as s - m with m
+  // the lane's current base (negm = -m broadcast is every score chain's
+  // accumulator start).  The base moves only when a tile's max exceeds it by
+  // more than 8 (a rare, wave-uniform branch), so P <= 2^8 stays exact in
+  // fp16.  The next tile's scores are issued before this tile's softmax; when
+  // that softmax moves the base it re-bases them too.
+  float l_run = 0.0f;
+  f32x16 negm;
   f32x16 o[2];
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
@@ -399,40 +427,62 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     o[1][e] = 0.0f;
   }
 
-  // softmax of one tile's scores into fp16 P (see the lazy-rescale note above)
-  auto softmax = [&](f32x16 (&sv)[2], f16x8 (&pf)[4]) {
+  // p = 2^s of the 16 scores of one key block into two P fragments
+  auto exp_block = [&](const f32x16& sk, f16x8& p0, f16x8& p1) {
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const f16x2 hr = f16x2{(f16)__builtin_amdgcn_exp2f(sk[e]), (f16)__builtin_amdgcn_exp2f(sk[e + 1])};
+      f16x8& d8 = e < 8 ? p0 : p1;
+      d8[e & 7] = hr[0];
+      d8[(e & 7) + 1] = hr[1];
+    }
+  };
+  // softmax of one tile's (shifted) scores sv into fp16 P; sn, when given,
+  // holds the next tile's scores, already issued against the current base.
+  // The exponentials of key block 0 are taken before the growth check (held
+  // there by an empty asm that reads them), so they run under the next
+  // tile's score MFMAs; the rare growth branch redoes them.
+  auto softmax = [&](f32x16 (&sv)[2], f16x8 (&pf)[4], f32x16* sn, bool first) {
     float mt = sv[0][0];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sv[kb][e]);
+    exp_block(sv[0], pf[0], pf[1]);
+    asm volatile("" ::"v"(pf[0]), "v"(pf[1]));
     mt = fa_max_halves(mt);
-    const bool grow = (mt - m_run) * p.c > 8.0f;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    // the first tile (base 0) also re-bases downwards, so a row whose scores
+    // are all far below 0 cannot underflow every p
+    if (__builtin_amdgcn_ballot_w64(mt > 8.0f || (first && mt < -8.0f)) != 0) {
       asm volatile("" ::: "memory");  // a real branch: never evaluated speculatively
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * p.c);
-      m_run = m_new;
+      const float d = first ? mt : fmaxf(mt, 0.0f);
+      const float alpha = __builtin_amdgcn_exp2f(-d);
       l_run *= alpha;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         o[0][e] *= alpha;
         o[1][e] *= alpha;
+        negm[e] -= d;
       }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sv[kb][e] -= d;
+      if (sn) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sn[kb][e] -= d;
+      }
+      exp_block(sv[0], pf[0], pf[1]);
     }
-    const float mc = m_run * p.c;
+    exp_block(sv[1], pf[2], pf[3]);
     float lsum = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][e], p.c, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][e + 1], p.c, -mc));
-        const f16x2 hr = f16x2{(f16)p0, (f16)p1};
-        pf[kb * 2 + (e >> 3)][e & 7] = hr[0];
-        pf[kb * 2 + (e >> 3)][(e & 7) + 1] = hr[1];
-        lsum = __builtin_amdgcn_fdot2(hr, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
-      }
+      for (int t = 0; t < 8; t += 2)
+        lsum = __builtin_amdgcn_fdot2(f16x2{pf[j][t], pf[j][t + 1]}, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
     l_run += lsum;
   };
   // O^T += V^T P^T over four 16-key steps (step j: tile keys 16j + 8g + [0, 8))
@@ -470,11 +520,14 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 2 < nkt) issue(nn, kt + 2);
     const unsigned char DLM_LDS* st = smem + c * FA_STAGE;
-    scores(smem + nxt * FA_STAGE, sn);  // tile kt+1, in the shadow of the softmax below
+    scores(smem + nxt * FA_STAGE, sn, negm);  // tile kt+1, in the shadow of the softmax below
     f16x8 vf[8];
     vread(st, vf);
     f16x8 pf[4];
-    softmax(sc, pf);  // tiles before the last are full: no mask
+    // the instruction mix of the block up to the growth branch, interleaved:
+    // the K fragments of the first k-step, then per score MFMA one more
+    // fragment read and five VALU (max, exponentials, converts)
+    softmax(sc, pf, sn, kt == 0);  // tiles before the last are full: no mask
     pv(vf, pf);
   };
   int cur = 0;  // ring position of the current tile
@@ -497,13 +550,17 @@ __global__ void __launch_bounds__(NWV * 64) flash_vt_pipe_kernel(FlashVtParams p
     f16x8 vf[8];
     vread(smem + cur * FA_STAGE, vf);
     f16x8 pf[4];
-    softmax(sc, pf);
+    softmax(sc, pf, nullptr, kt == 0);
     pv(vf, pf);
   };
   // two tiles per iteration with the score buffers swapping roles, so no
   // loop-carried copy of the next tile's 32 scores is needed
   f32x16 sa[2], sb[2];
-  scores(smem, sa);
+  // the base starts at 0: tile 0's softmax moves it to that tile's max when
+  // the max lies outside [-8, 8]
+#pragma unroll
+  for (int e = 0; e < 16; ++e) negm[e] = 0.0f;
+  scores(smem, sa, negm);
   int kt = 0;
   // six tiles per iteration: the ring position and the score buffers both
   // come back to where they started, so every LDS address in the body is a

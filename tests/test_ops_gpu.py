@@ -388,6 +388,41 @@ def test_attention_vt(gpu, B, H, Sq, Sk):
     assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), "attention_vt")
 
 
+@pytest.mark.parametrize("mode,B,H,Sq,Sk", [("wide", 2, 4, 1024, 1024), ("wide", 1, 2, 130, 97),
+                                            ("negative", 2, 4, 1024, 1024), ("negative", 1, 2, 300, 77),
+                                            ("negative", 1, 2, 130, 33), ("growing", 1, 2, 256, 1000)])
+def test_attention_vt_rebase_paths(gpu, mode, B, H, Sq, Sk):
+    """The flash kernel's running base in the online softmax: scores with a
+    spread of ~11 in the exponent's units (the base moves whenever a tile's
+    max passes it by more than 2^8), scores that are all far below 0 (the
+    first tile moves the base down, or every p would underflow in fp16),
+    and keys whose scores grow along the sequence (a move on many tiles).
+    Same bar as every attention case."""
+    Dh = 64
+    C = H * Dh
+    announce(f"attention_vt rebase {mode} B={B} H={H} Sq={Sq} Sk={Sk}")
+    q, k, v = randn((B, H, Sq, Dh), 130), randn((B, H, Sk, Dh), 131), randn((B, H, Sk, Dh), 132)
+    if mode == "wide":
+        q = (q * 8).half().float()
+    elif mode == "negative":
+        q = (1.0 + 0.1 * q).half().float()
+        k = (-1.5 + 0.3 * k).half().float()
+    else:  # key j's score against a query grows like 2 j / Sk in raw units
+        q = (0.5 + 0.1 * q).half().float()
+        k = (torch.linspace(0.0, 2.0, Sk).reshape(1, 1, Sk, 1) + 0.1 * k).half().float()
+    dq = to_gpu(q.permute(0, 2, 1, 3).reshape(B, Sq, C))
+    dk = to_gpu(k.permute(0, 2, 1, 3).reshape(B, Sk, C))
+    ld = (Sk + 7) // 8 * 8
+    vt = torch.zeros(B, H, Dh, ld, dtype=torch.float16, device=gpu)
+    vt[..., :Sk] = to_gpu(v.transpose(2, 3).contiguous())
+    o = torch.empty(B, Sq, C, dtype=torch.float16, device=gpu)
+    ops.attention_vt(dq, dk, vt, o, B=B, H=H, Sq=Sq, Sk=Sk, q_strides=(Sq * C, C, Dh),
+                     k_strides=(Sk * C, C, Dh), vt_strides=(H * Dh * ld, Dh * ld), vt_ld=ld,
+                     o_strides=(Sq * C, C, Dh), scale=0.125)
+    ref = torch.cat([R.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], 0.125) for b in range(B)])
+    assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), f"attention_vt {mode}")
+
+
 @pytest.mark.parametrize("M,N,K,act,vt", [
     (2048, 1280, 1280, 0, False), (8192, 640, 640, 0, False), (2048, 3840, 1280, 0, True),
     (8192, 1920, 640, 0, True), (2048, 10240, 1280, 4, False), (8192, 5120, 640, 4, False),
