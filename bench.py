@@ -55,6 +55,10 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB (5 times), to scale the "
                          "FETCH_SIZE / WRITE_SIZE counters of a PMC run")
+    ap.add_argument("--calibrate-mfma", action="store_true",
+                    help="only run the MFMA calibration kernel (register-only fp16 MFMA "
+                         "stream of known FLOPs, 5 launches) and print its measured rate, to "
+                         "read the MFMA counters of a PMC run against")
     return ap.parse_args()
 
 
@@ -69,6 +73,33 @@ def calibrate_copy():
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"calibrate_copy_bytes_per_dispatch": 2 * n}), flush=True)
+
+
+def calibrate_mfma():
+    """The library's MFMA calibration kernel (dlm_mfma_probe): 1024
+    workgroups of 4 waves (4 waves per SIMD), each wave 4000 rounds of eight
+    32x32x16 fp16 MFMAs on registers.  Prints FLOPs per launch and the rate of
+    each of 5 launches timed with device events on the launch stream."""
+    import ctypes
+    import torch
+    from dollama_amd import _lib
+    blocks, iters = 1024, 4000
+    flop = blocks * 4 * iters * 8 * 32768
+    out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda:0")
+    st = torch.cuda.current_stream()
+    rates = []
+    for _ in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        _lib.call("dlm_mfma_probe", blocks, iters, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st.cuda_stream))
+        e1.record(st)
+        torch.cuda.synchronize()
+        rates.append(flop / (e0.elapsed_time(e1) * 1e-3))
+    rates = rates[1:]  # the first launch warms the clocks
+    print(json.dumps({"calibrate_mfma_flop_per_dispatch": flop,
+                      "tflops": [round(r / 1e12, 1) for r in rates],
+                      "frac_of_peak": [round(r / MFMA_FP16_PEAK, 4) for r in rates],
+                      "finite": bool(torch.isfinite(out).all())}), flush=True)
 
 
 def measured_traffic():
@@ -351,6 +382,9 @@ def main():
     args = parse()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.calibrate_mfma:
+        calibrate_mfma()
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the UNet step "

@@ -136,6 +136,9 @@ HIP_SIGNATURES = {
     "dlm_gemm_override_shape": (I, [I, I, I, I, I]),
     "dlm_gemm_force_split": (I, [I]),
     "dlm_gemm_set_variant": (I, [I]),
+    "dlm_mfma_probe": (I, [I, I, P, P]),
+    "dlm_scratch_release": (I, [P]),
+    "dlm_scratch_bytes": (I, [POINTER(c_size_t)]),
 }
 
 

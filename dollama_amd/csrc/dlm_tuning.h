@@ -42,6 +42,13 @@ int dlm_gemm_force_split(int splits);
  * splits for 256x160 grids that fill the chip). */
 int dlm_gemm_set_variant(int variant);
 
+/* Counter calibration: `blocks` workgroups of 4 waves, each wave `iters`
+ * rounds of eight v_mfma_f32_32x32x16_f16 on register operands (no memory
+ * traffic in the loop): blocks * 4 * iters * 8 * 32768 FLOP per launch,
+ * from which a profiler's MFMA counters can be read against a known rate.
+ * out receives blocks * 256 floats. */
+int dlm_mfma_probe(int blocks, int iters, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

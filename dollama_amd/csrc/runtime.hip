@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "dlm_tuning.h"
 
 namespace dlm {
 
@@ -161,9 +162,47 @@ size_t scratch_bytes() {
   return t;
 }
 
+// Counter calibration kernel: every wave issues `iters` rounds of eight
+// v_mfma_f32_32x32x16_f16 on four independent accumulators, operands in
+// registers and no memory traffic in the loop (8 x 32768 FLOP per round), so
+// a profiler's MFMA counters can be read against a known MFMA rate.
+__global__ void __launch_bounds__(256) mfma_probe_kernel(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  f16x8 a, b;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    a[t] = (f16)(0.001f * (float)(lane + t));
+    b[t] = (f16)(0.002f * (float)(lane - t));
+  }
+  f32x16 c0{}, c1{}, c2{}, c3{};
+  for (int i = 0; i < iters; ++i) {
+    c0 = mfma32x32x16(a, b, c0);
+    c1 = mfma32x32x16(b, a, c1);
+    c2 = mfma32x32x16(a, a, c2);
+    c3 = mfma32x32x16(b, b, c3);
+    c0 = mfma32x32x16(a, b, c0);
+    c1 = mfma32x32x16(b, a, c1);
+    c2 = mfma32x32x16(a, a, c2);
+    c3 = mfma32x32x16(b, b, c3);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sum += c0[e] + c1[e] + c2[e] + c3[e];
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = sum;
+}
+
 }  // namespace dlm
 
 extern "C" {
+
+int dlm_mfma_probe(int blocks, int iters, float* out, void* stream) {
+  if (blocks <= 0 || iters <= 0) return DLM_OK;
+  DLM_REQUIRE(out != nullptr, "out is NULL");
+  DLM_LAUNCH("mfma_probe_kernel", dlm::mfma_probe_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+             out, iters);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
 
 const char* dlm_last_error(void) { return dlm::g_last_error.c_str(); }
 
