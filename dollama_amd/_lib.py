@@ -99,6 +99,7 @@ HIP_SIGNATURES = {
     "dlm_geglu_fp16": (I, [P, P, I, I, P]),
     "dlm_silu_fp16": (I, [P, P, I, P]),
     "dlm_gelu_fp16": (I, [P, P, I, P]),
+    "dlm_gelu_tanh_fp16": (I, [P, P, I, P]),
     "dlm_add_fp16": (I, [P, P, P, I, P]),
     "dlm_upsample_nearest2x_fp16": (I, [P, P, I, I, I, I, P]),
     "dlm_bias_add_rowvec_fp16": (I, [P, P, P, I, I, P]),

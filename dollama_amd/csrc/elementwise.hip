@@ -27,6 +27,16 @@ __global__ void gelu_kernel(const f16* in, f16* out, long long n) {
   GRID_STRIDE(i, n) out[i] = (f16)gelu_erf_f((float)in[i]);
 }
 
+// GELU, tanh approximation: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+// in fp32 (reference gelu_tanh_fp16, src/kernels/activation.cu:54-70)
+__global__ void gelu_tanh_kernel(const f16* in, f16* out, long long n) {
+  GRID_STRIDE(i, n) {
+    const float x = (float)in[i];
+    const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    out[i] = (f16)(0.5f * x * (1.0f + tanhf(inner)));
+  }
+}
+
 __global__ void add_kernel(const f16* a, const f16* b, f16* out, long long n) {
   GRID_STRIDE(i, n) out[i] = (f16)((float)a[i] + (float)b[i]);
 }
@@ -247,6 +257,15 @@ int dlm_gelu_fp16(const void* in, void* out, int n, void* stream) {
   DLM_REQUIRE(in && out, "NULL pointer");
   DLM_LAUNCH("gelu_kernel", gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)in, (f16*)out,
                      (long long)n);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int dlm_gelu_tanh_fp16(const void* in, void* out, int n, void* stream) {
+  EW_PRE(n);
+  DLM_REQUIRE(in && out, "NULL pointer");
+  DLM_LAUNCH("gelu_tanh_kernel", gelu_tanh_kernel, dim3(grid_for(n)), dim3(256), 0, s_, (const f16*)in,
+             (f16*)out, (long long)n);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

@@ -177,6 +177,11 @@ def launch_gelu(d_in, d_out, n):
     _unary("dlm_gelu_fp16", d_in, d_out, n)
 
 
+def launch_gelu_tanh(d_in, d_out, n):
+    """Reference launch_gelu_tanh (src/kernels/activation.cuh:41)."""
+    _unary("dlm_gelu_tanh_fp16", d_in, d_out, n)
+
+
 def launch_add(d_a, d_b, d_out, n):
     """reference src/kernels/elementwise.cuh:26."""
     if n <= 0:

@@ -192,9 +192,13 @@ int dlm_attention_fp16(const void* q, const void* k, const void* v, void* out,
  * Replaces launch_geglu (src/kernels/geglu.cuh:42). */
 int dlm_geglu_fp16(const void* in, void* out, int tokens, int d, void* stream);
 
-/* Replace launch_silu / launch_gelu (src/kernels/activation.cuh:33-37). */
+/* Replace launch_silu / launch_gelu / launch_gelu_tanh
+ * (src/kernels/activation.cuh:33-41): x sigmoid(x), 0.5 x (1 + erf(x/sqrt 2)),
+ * 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); fp32 math, in place
+ * allowed. */
 int dlm_silu_fp16(const void* in, void* out, int n, void* stream);
 int dlm_gelu_fp16(const void* in, void* out, int n, void* stream);
+int dlm_gelu_tanh_fp16(const void* in, void* out, int n, void* stream);
 /* Replace launch_add / launch_upsample_nearest2x (src/kernels/elementwise.cuh:26-37). */
 int dlm_add_fp16(const void* a, const void* b, void* out, int n, void* stream);
 int dlm_upsample_nearest2x_fp16(const void* in, void* out, int N, int C, int H, int W,

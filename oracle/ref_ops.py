@@ -52,6 +52,12 @@ def gelu_erf(x):
     return 0.5 * x * (1.0 + torch.erf(x * (1.0 / math.sqrt(2.0))))
 
 
+def gelu_tanh(x):
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (src/kernels/activation.cu:54-70,
+    src/tests/test_activation.cu:127-131)."""
+    return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
 def layer_norm(x, gamma, beta, eps=1e-5):
     """LayerNorm over the last dim (src/kernels/layernorm.cu:78-126)."""
     C = x.shape[-1]

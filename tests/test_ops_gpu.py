@@ -492,6 +492,11 @@ def test_elementwise_ops(gpu):
     assert_close(out, R.silu(a), "silu")
     ops.launch_gelu(to_gpu(a), out, n)
     assert_close(out, R.gelu_erf(a), "gelu")
+    ops.launch_gelu_tanh(to_gpu(a), out, n)
+    assert_close(out, R.gelu_tanh(a), "gelu_tanh")
+    inplace = to_gpu(a)
+    ops.launch_gelu_tanh(inplace, inplace, n)
+    assert torch.equal(inplace, out), "gelu_tanh in place"
     ops.launch_add(to_gpu(a), to_gpu(b), out, n)
     assert_close(out, a + b, "add")
     x = randn((2, 3, 5, 7), 122)

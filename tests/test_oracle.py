@@ -225,6 +225,20 @@ def test_activation_known_values():
     _close(naive.gelu_erf(x.numpy()), R.gelu_erf(x), 1e-6)
 
 
+def test_gelu_tanh_oracle():
+    """The tanh-approximate GELU (src/tests/test_activation.cu:127-131, 276-284)
+    against torch's own approximate='tanh' GELU, its odd-part identity
+    f(x) - f(-x) = x, f(0) = 0, and its departure from the erf form (a few
+    1e-4 near |x| = 2.5, so a swapped formula is caught)."""
+    x = _rand((257,), 31, 3.0)
+    _close(R.gelu_tanh(x), torch.nn.functional.gelu(x, approximate="tanh"), 1e-6)
+    _close(R.gelu_tanh(x) - R.gelu_tanh(-x), x, 1e-5)
+    assert float(R.gelu_tanh(torch.tensor([0.0]))[0]) == 0.0
+    d = float((R.gelu_tanh(torch.tensor([2.5], dtype=torch.float64))
+               - R.gelu_erf(torch.tensor([2.5], dtype=torch.float64)))[0])
+    assert 3e-4 < d < 6e-4
+
+
 def test_geglu_known_and_random():
     """src/tests/test_geglu.cu:130-160: [1, -1, 1, 0] -> [gelu(1), -gelu(0)] = [0.8413, 0];
     value is the first half, gate the second."""
