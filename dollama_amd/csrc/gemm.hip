@@ -1777,9 +1777,16 @@ static int launch_gemm_impl(const Desc& ad, const RowDesc& bd, const EpiArgs& ep
       case 39: return launch_dma<128, 64, 64, 32, 3, false, 2>(ad, bd, ep, M, N, s);
       case 40: return launch_dma<128, 128, 32, 64, 2, true>(ad, bd, ep, M, N, s);
       case 41: return launch_dma<256, 160, 32, 160, 3, true>(ad, bd, ep, M, N, s);
+      case 42: return launch_dma<128, 16, 16, 16, 3>(ad, bd, ep, M, N, s);
+      case 43: return launch_dma<64, 16, 16, 16, 3>(ad, bd, ep, M, N, s);
       default: break;
     }
     if (g_forced_tile == 0) {
+      // at most 16 output columns (the UNet's conv_out, 4 channels): one
+      // 16-column block per wave, 8 waves of 16 rows, instead of a 64-column
+      // tile that is mostly padding
+      if (N <= 16 && !ep.vt && ep.act != DLM_ACT_GEGLU && ceil_div(M, 128) >= kCUs / 2)
+        return launch_dma<128, 16, 16, 16, 3>(ad, bd, ep, M, N, s);
       // Measured on the UNet's shapes (warmed-up clocks, N(0,1) data):
       // 8-wave tiles (two waves per SIMD) everywhere.  128x128 tiles: two
       // slices in flight when two workgroups share a CU, four when the grid
@@ -2641,7 +2648,7 @@ extern "C" int dlm_gemm_force_split(int splits) {
 }
 
 extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int splits) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 41 && splits >= 0 && splits <= 64, "bad tile / split");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 43 && splits >= 0 && splits <= 64, "bad tile / split");
   if (M == 0 && N == 0 && K == 0) {
     dlm::g_overrides.clear();
     return DLM_OK;
@@ -2657,7 +2664,7 @@ extern "C" int dlm_gemm_override_shape(int M, int N, int K, int tile_id, int spl
 }
 
 extern "C" int dlm_gemm_force_tile(int tile_id) {
-  DLM_REQUIRE(tile_id >= 0 && tile_id <= 41, "tile_id must be in [0, 41]");
+  DLM_REQUIRE(tile_id >= 0 && tile_id <= 43, "tile_id must be in [0, 43]");
   dlm::g_forced_tile = tile_id;
   return DLM_OK;
 }

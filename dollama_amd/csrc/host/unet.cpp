@@ -12,6 +12,10 @@
 
 namespace dollama {
 
+// Input channels of conv_in after padding (the latent's 4 channels, zero
+// filled): a multiple of 64 puts the conv on the DMA implicit-GEMM core.
+static constexpr int kConvInPad = 64;
+
 // Launch one C-ABI kernel call; when profiling, its kernels carry an event
 // pair in their own dispatches (dlm_prof_arm).
 #define LAUNCH(cls, flops, bytes, expr)          \
@@ -164,7 +168,8 @@ UNet::UNet(const UNetConfig& cfg) : cfg_(cfg) {
   if (c.head_dim != 64) throw std::invalid_argument("UNet: head_dim must be 64");
   if (c.cross_dim % 8 || c.text_dim % 8 || c.id_dim % 8)
     throw std::invalid_argument("UNet: cross/text/id dims must be multiples of 8");
-  if (c.in_channels > 8) throw std::invalid_argument("UNet: in_channels > 8 not supported");
+  if (c.in_channels > kConvInPad)
+    throw std::invalid_argument("UNet: more than 64 input channels not supported");
 }
 
 UNet::~UNet() {
@@ -557,7 +562,10 @@ void UNet::pack_all(void* stream) {
   kv_total_ = 0;
   tproj_total_ = 0;
   cursor_ = 0;
-  conv_in_ = pack_conv("conv_in.", c.C0, c.in_channels, 3, 8, stream);
+  // the latent's channels padded to 64: the conv then runs on the DMA core's
+  // implicit GEMM (K = 9 x 64) instead of the register-staged small-channel
+  // kernel
+  conv_in_ = pack_conv("conv_in.", c.C0, c.in_channels, 3, kConvInPad, stream);
   te1w_ = copy_of("time_embedding.linear_1.weight", {T, c.C0}, stream);
   te1b_ = copy_of("time_embedding.linear_1.bias", {T}, stream);
   te2w_ = copy_of("time_embedding.linear_2.weight", {T, T}, stream);
@@ -1121,11 +1129,11 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
 
   size_t ri = 0, ai = 0;
   std::vector<std::pair<void*, int>> skips;
-  // ---- conv_in (latent NCHW -> channels-last, padded to 8 channels)
-  void* xin = P((size_t)B * HW0 * 8);
-  LAUNCH(kOther, 0.0, 0.0, dlm_nchw_to_nhwc_fp16(latent, xin, B, c.in_channels, HW0, 8, stream));
+  // ---- conv_in (latent NCHW -> channels-last, zero-padded to 64 channels)
+  void* xin = P((size_t)B * HW0 * kConvInPad);
+  LAUNCH(kOther, 0.0, 0.0, dlm_nchw_to_nhwc_fp16(latent, xin, B, c.in_channels, HW0, kConvInPad, stream));
   void* cur = P((size_t)B * HW0 * C0);
-  conv3(conv_in_, xin, 8, nullptr, 0, cur, C0, B, H, W, 1, false, stream, c.in_channels);
+  conv3(conv_in_, xin, kConvInPad, nullptr, 0, cur, C0, B, H, W, 1, false, stream, c.in_channels);
   stage("conv_in_out", cur, (size_t)B * HW0 * C0, C0, stream);
   skips.push_back({cur, C0});
 

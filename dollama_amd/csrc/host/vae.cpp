@@ -12,6 +12,10 @@
 
 namespace dollama {
 
+// Channels of post_quant_conv's output as conv_in reads it (the latent's 4,
+// zero-padded): a multiple of 64 puts conv_in on the DMA implicit-GEMM core.
+static constexpr int kPqPad = 64;
+
 #define LAUNCH(cls, flops, bytes, expr)          \
   do {                                           \
     prof_begin((cls), (flops), (bytes), stream); \
@@ -295,7 +299,9 @@ void VAE::pack_all(void* stream) {
   cursor_ = 0;
   const int L = c.latent_channels, Cm = c.up_ch(0);
   pqc_ = pack_conv("post_quant_conv.", L, L, 1, 8, 1.0f, stream);
-  conv_in_ = pack_conv("decoder.conv_in.", Cm, L, 3, 8, 1.0f, stream);
+  // conv_in reads post_quant_conv's output zero-padded to 64 channels, so it
+  // runs on the DMA implicit-GEMM core (K = 9 x 64)
+  conv_in_ = pack_conv("decoder.conv_in.", Cm, L, 3, kPqPad, 1.0f, stream);
   res_.clear();
   ups_.clear();
   res_.push_back(pack_resnet("decoder.mid_block.resnets.0.", Cm, Cm, false, false, stream));
@@ -517,16 +523,17 @@ void VAE::decode(int N, int h, int w, const void* latent, void* image, void* str
   DeviceArenaScope scope(DeviceArenaId::VAE);
   void* A = scope.alloc_bytes(carry);
   void* B = scope.alloc_bytes(carry);
-  // latent NCHW -> channels-last, 8 channels (zero padded)
+  // latent NCHW -> channels-last, 8 channels (zero padded); post_quant_conv's
+  // output zero-padded to 64 channels for conv_in
   {
     DeviceArenaScope sc(DeviceArenaId::VAE);
     void* x8 = sc.alloc<uint16_t>((size_t)N * HW0 * 8);
-    void* pq = sc.alloc<uint16_t>((size_t)N * HW0 * 8);
+    void* pq = sc.alloc<uint16_t>((size_t)N * HW0 * kPqPad);
     LAUNCH(kOther, 0.0, 0.0, dlm_nchw_to_nhwc_fp16(latent, x8, N, L, HW0, 8, stream));
-    DLM_CALL(dlm_memset_async(pq, 0, (size_t)N * HW0 * 8 * kH, stream));
-    conv(pqc_, x8, 8, 8, pq, L, 8, false, N, h, w, 1, false, stream);
-    stage("post_quant_conv_out", pq, (size_t)N * HW0 * 8, 8, false, stream);
-    conv(conv_in_, pq, 8, 8, A, Cm, Cm, false, N, h, w, 3, false, stream);
+    DLM_CALL(dlm_memset_async(pq, 0, (size_t)N * HW0 * kPqPad * kH, stream));
+    conv(pqc_, x8, 8, 8, pq, L, kPqPad, false, N, h, w, 1, false, stream);
+    stage("post_quant_conv_out", pq, (size_t)N * HW0 * kPqPad, kPqPad, false, stream);
+    conv(conv_in_, pq, kPqPad, kPqPad, A, Cm, Cm, false, N, h, w, 3, false, stream);
   }
   stage("conv_in_out", A, (size_t)N * HW0 * Cm, Cm, false, stream);
   // mid block

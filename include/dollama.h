@@ -215,7 +215,7 @@ int dlm_vae_decode(void* handle, int N, int h, int w, const void* latent, void* 
                    void* stream);
 
 /* Stage hook for tests (the reference's golden stages, src/tests/
- * test_vae_decode.cu): post_quant_conv_out (8 channels, the last 4 zero),
+ * test_vae_decode.cu): post_quant_conv_out (64 channels, the last 60 zero),
  * conv_in_out, mid_block_out, up_block_{0..3}_out (channels-last, fp32
  * when is_f32), final_image (NCHW fp16). */
 typedef void (*dlm_vae_stage_hook)(const char* name, const void* dptr, size_t n, int C,
