@@ -41,6 +41,7 @@ class ConvNhwcArgs(ctypes.Structure):
         ("residual", P), ("res_ld", I),
         ("out", P), ("ldy", I), ("out_nchw", I), ("act", I),
         ("out_f32", I), ("res_f32", I),
+        ("gn_stats", P),
     ]
 
 
@@ -108,6 +109,7 @@ HIP_SIGNATURES = {
     "dlm_conv_bias_residual_fp16": (I, [P, P, P, P, I, I, I, I, P]),
     "dlm_timestep_embedding_fp16": (I, [P, F, I, F, P]),
     "dlm_linear_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, F, F, I, P]),
+    "dlm_linear_gn_stats_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, F, F, I, I, P, P]),
     "dlm_geglu_pack_fp16": (I, [P, P, P, P, I, I, P]),
     "dlm_conv_weight_pack_fp16": (I, [P, P, I, I, I, I, I, I, I, P]),
     "dlm_nchw_to_nhwc_fp16": (I, [P, P, I, I, I, I, P]),
@@ -128,6 +130,8 @@ HIP_SIGNATURES = {
     "dlm_scale_latent_fp16": (I, [P, P, I, F, I, P]),
     "dlm_linear_f32out_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, F, F, I, P]),
     "dlm_group_norm_nhwc_f32in": (I, [P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
+    "dlm_group_norm_nhwc_prestats_fp16": (I, [P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
+    "dlm_group_norm_chunk_stats_fp16": (I, [P, I, I, I, I, P, P]),
     "dlm_cast_f32_to_f16": (I, [P, P, LL, F, P]),
     "dlm_scale_fp16": (I, [P, LL, F, P]),
     "dlm_latent_to_vae_fp16": (I, [P, P, LL, F, P]),

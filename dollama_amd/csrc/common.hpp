@@ -89,6 +89,28 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// GroupNorm chunk statistics, one definition for every producer (the
+// statistics pass over a tensor, and GEMM / conv epilogues that write them
+// for their own output), so they agree bit for bit and a sample's statistics
+// never depend on the batch or on the kernel that computed them.
+// Chunk k of a sample is its pixel rows [64k, min(64k + 64, HW)).  Per
+// channel, over the chunk's rows in ascending order, with shift = the
+// chunk's first value:
+//   d = x - shift;  s1 = s1 + d;  s2 = fma(d, d, s2)
+// and then (mean, M2) = (shift + s1 / cnt, max(s2 - s1 (s1 / cnt), 0)).
+// Stored as float2 [N][chunks][C].
+constexpr int kGnChunk = 64;
+__device__ __forceinline__ void gn_stat_add(float x, float shift, float& s1, float& s2) {
+  const float d = x - shift;
+  s1 = s1 + d;
+  s2 = __builtin_fmaf(d, d, s2);
+}
+__device__ __forceinline__ float2 gn_stat_finish(float s1, float s2, float shift, int cnt) {
+  // a whole chunk divides by 64 exactly as a multiply, whatever the division lowering
+  const float md = cnt == kGnChunk ? s1 * (1.0f / kGnChunk) : s1 / (float)cnt;
+  return make_float2(shift + md, fmaxf(__builtin_fmaf(-s1, md, s2), 0.0f));
+}
+
 // Grid of a grid-stride elementwise launch over n items.
 static inline int grid_for(long long n, int threads = 256, int cap = 8192) {
   return (int)std::max<long long>(1, std::min<long long>((n + threads - 1) / threads, cap));
@@ -116,6 +138,9 @@ int scratch_release(hipStream_t stream);
 size_t scratch_bytes();
 int split_workspace_release(hipStream_t stream);
 size_t split_workspace_bytes();
+// GroupNorm chunk statistics (kGnChunk) of fp16 channels-last x [N, HW, C]
+// (row stride ld) into stats [N][chunks][C] (norm.hip).
+int gn_chunk_stats(const void* x, int ld, int N, int HW, int C, float2* stats, hipStream_t s);
 // Name of the kernel an entry point launches last (per thread), for
 // per-kernel timing attribution (dlm_last_kernel).
 void note_kernel(const char* name);

@@ -81,6 +81,12 @@ struct EpiArgs {
   const float* ln_c2;
   float ln_invk;
   float ln_eps;
+  // GroupNorm chunk statistics of the fp16 output (common.hpp): written to
+  // gn_stats[n][chunk][col] when non-null, gn_hw output rows per sample (a
+  // multiple of 64), gn_chunks = gn_hw / 64
+  float2* gn_stats;
+  int gn_hw;
+  int gn_chunks;
 };
 
 // ---------------------------------------------------------------------------
@@ -843,7 +849,7 @@ __device__ __forceinline__ void epi4_geglu(const f32x4& a, int row, int col, con
 // once; per block, the loads, guards and stores of epi4 (one round trip per
 // operand and block) made the epilogue several times longer.  The arithmetic
 // is epi4's, in the same order.
-__device__ __forceinline__ bool epi_tile_fast(const EpiArgs& ep) {
+__host__ __device__ __forceinline__ bool epi_tile_fast(const EpiArgs& ep) {
   return !ep.y_f32 && !ep.res_f32 && !ep.out_nchw && !ep.vt;
 }
 
@@ -867,9 +873,13 @@ __device__ __forceinline__ void epi_tile_early(int row0, int col0, const EpiArgs
 }
 
 // EARLY: bias and residual already in bv / rv (epi_tile_early).
+// to_lds: stl is this lane's position in an LDS copy of the workgroup's
+// output tile (row stride sld halfs), which receives the stored fp16 values
+// (a flag, not a null test: LDS address 0 is a valid position).
 template <int TM, int TN, bool EARLY = false>
 __device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, int col0, const EpiArgs& ep,
-                                         f16x4 (&bv)[TN], f16x4 (&rv)[TM][TN]) {
+                                         f16x4 (&bv)[TN], f16x4 (&rv)[TM][TN], bool to_lds = false,
+                                         f16 DLM_LDS* stl = nullptr, int sld = 0) {
   f16x4 tv[TM][TN];
   if (!EARLY && ep.bias) {
 #pragma unroll
@@ -920,11 +930,32 @@ __device__ __forceinline__ void epi_tile(const f32x4 (&acc)[TM][TN], int row0, i
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[t] += ep.beta * (float)rv[i][j][t];
       }
-      if (row < ep.M && col < ep.N) {
-        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-        *reinterpret_cast<f16x4*>(ep.y + (size_t)row * ep.ldy + col) = o;
-      }
+      const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+      if (row < ep.M && col < ep.N) *reinterpret_cast<f16x4*>(ep.y + (size_t)row * ep.ldy + col) = o;
+      if (to_lds) *reinterpret_cast<f16x4 DLM_LDS*>(stl + i * 16 * sld + j * 16) = o;
     }
+  }
+}
+
+// GroupNorm chunk statistics (common.hpp) of a BM x BN output tile held in
+// LDS (row stride BN): one thread per (64-row chunk, column), the chunk's
+// rows in ascending order.  Needs ep.gn_hw % 64 == 0, so a chunk that starts
+// inside M lies inside it.
+template <int BM, int BN>
+__device__ __forceinline__ void gn_tile_stats(const f16 DLM_LDS* st, int m0, int n0, const EpiArgs& ep,
+                                              int tid, int nt) {
+  constexpr int PAIRS = (BM / kGnChunk) * BN;
+  for (int p = tid; p < PAIRS; p += nt) {
+    const int kk = p / BN, c = p - kk * BN;
+    const int grow = m0 + kk * kGnChunk, gcol = n0 + c;
+    if (grow >= ep.M || gcol >= ep.N) continue;
+    const f16 DLM_LDS* col = st + kk * kGnChunk * BN + c;
+    const float shift = (float)col[0];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll 16
+    for (int r = 0; r < kGnChunk; ++r) gn_stat_add((float)col[r * BN], shift, s1, s2);
+    const int n = grow / ep.gn_hw, k = (grow - n * ep.gn_hw) / kGnChunk;
+    ep.gn_stats[((size_t)n * ep.gn_chunks + k) * ep.N + gcol] = gn_stat_finish(s1, s2, shift, kGnChunk);
   }
 }
 
@@ -1450,11 +1481,22 @@ dma_gemm_kernel(Desc ad, RowDesc bd, EpiArgs ep, int tiles_m, int tiles_n, Split
       return;
     }
     if (epi_tile_fast(ep)) {
+      // GroupNorm statistics of the output: the tile's fp16 values are copied
+      // into the (now free) operand ring and reduced from there
+      static_assert(BM * BN * 2 <= NS * STAGE, "output tile larger than the LDS ring");
+      f16 DLM_LDS* stile = (f16 DLM_LDS*)smem;
+      f16 DLM_LDS* stl = stile + (wm * WM + (lane & 15)) * BN + wn * WN + 4 * (lane >> 4);
+      const bool gn = ep.gn_stats != nullptr;
+      if (gn) __syncthreads();  // every wave is done with the ring
       if (early) {
-        epi_tile<TM, TN, true>(acc, row0, col0, ep, ebv, erv);
+        epi_tile<TM, TN, true>(acc, row0, col0, ep, ebv, erv, gn, stl, BN);
       } else {
         f16x4 bv[TN], rv[TM][TN];
-        epi_tile<TM, TN>(acc, row0, col0, ep, bv, rv);
+        epi_tile<TM, TN>(acc, row0, col0, ep, bv, rv, gn, stl, BN);
+      }
+      if (ep.gn_stats) {
+        __syncthreads();
+        gn_tile_stats<BM, BN>(stile, m0, n0, ep, tid, NW * 64);
       }
       return;
     }
@@ -1487,10 +1529,17 @@ constexpr int kSplitCounters = 1 << 16;
 static std::mutex g_split_mu;
 static std::map<std::pair<int, hipStream_t>, SplitWorkspace> g_split_ws;
 
+// A stream under graph capture gets no new workspace (the allocation and its
+// synchronous clear would invalidate the capture): its launches run unsplit
+// until the stream has made one outside capture.
 static const SplitWorkspace* split_workspace(hipStream_t s) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lk(g_split_mu);
+  auto it = g_split_ws.find({dev, s});
+  if (it != g_split_ws.end() && it->second.ws) return &it->second;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
   SplitWorkspace& w = g_split_ws[{dev, s}];
   if (!w.ws) {
     float* ws = nullptr;
@@ -1586,10 +1635,22 @@ static const char* mfma_kernel_name() {
   return n.c_str();
 }
 
+// Set by a launch whose epilogue writes the requested GroupNorm statistics
+// (EpiArgs::gn_stats); a launch that cannot leaves it false and the entry
+// point runs the statistics pass instead.
+static thread_local bool t_gn_written = false;
+
 template <int BM, int BN, int WM, int WN, int NS, bool PF = false, int SPS = 1, class Desc>
-static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep, int M, int N,
+static int launch_dma(const Desc& ad, const RowDesc& bd, const EpiArgs& ep_in, int M, int N,
                       hipStream_t s, int S = 1) {
   static_assert(NS * SPS * (BM + BN) * BK * 2 <= 160 * 1024, "LDS ring larger than 160 KiB");
+  // the batched epilogue (wave tiles of at most 20 blocks) is the one that
+  // writes GroupNorm statistics
+  EpiArgs ep = ep_in;
+  const bool gn = ep.gn_stats && (WM / 16) * (WN / 16) <= 20 && epi_tile_fast(ep) &&
+                  ep.act != DLM_ACT_GEGLU && ep.gn_hw > 0 && ep.gn_hw % kGnChunk == 0;
+  if (!gn) ep.gn_stats = nullptr;
+  t_gn_written = gn;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
@@ -2191,7 +2252,13 @@ int conv_nhwc_impl(const dlm_conv_nhwc_args* a, const ConvGeom& g, hipStream_t s
   ep.out_nchw = a->out_nchw;
   ep.y_f32 = a->out_f32 ? 1 : 0;
   ep.res_f32 = a->res_f32 ? 1 : 0;
-  return launch_gemm(d, bd, ep, d.M, a->Cout, s);
+  ep.gn_stats = (float2*)a->gn_stats;
+  ep.gn_hw = d.HoWo;
+  ep.gn_chunks = (d.HoWo + kGnChunk - 1) / kGnChunk;
+  t_gn_written = false;
+  const int st = launch_gemm(d, bd, ep, d.M, a->Cout, s);
+  if (st != DLM_OK || !a->gn_stats || t_gn_written) return st;
+  return gn_chunk_stats(a->out, a->ldy, a->N, d.HoWo, a->Cout, (float2*)a->gn_stats, s);
 }
 
 }  // namespace dlm
@@ -2224,6 +2291,35 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
   }
   return linear_impl(X, lda, W, ldw, bias, R, ldr, Y, ldy, M, N, K, alpha, beta, act,
                      (hipStream_t)stream);
+}
+
+int dlm_linear_gn_stats_fp16(const void* X, int lda, const void* W, int ldw, const void* bias,
+                             const void* R, int ldr, void* Y, int ldy, int M, int N, int K, float alpha,
+                             float beta, int act, int tokens, void* gn_stats, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
+  DLM_REQUIRE(gn_stats, "gn_stats is NULL (use dlm_linear_fp16)");
+  DLM_REQUIRE(act != DLM_ACT_GEGLU, "gn_stats with a GEGLU output");
+  DLM_REQUIRE(tokens > 0 && M % tokens == 0 && tokens <= 65536, "M must be samples x tokens, tokens <= 65536");
+  DLM_REQUIRE(N % 8 == 0 && ldy % 8 == 0 && dlm_aligned16(Y) && dlm_aligned16(gn_stats),
+              "gn_stats needs N and ldy multiples of 8 and 16-byte aligned Y / gn_stats");
+  DLM_REQUIRE(X && W && Y, "NULL operand");
+  DLM_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0, "K, lda and ldw must be multiples of 8");
+  DLM_REQUIRE(lda >= K && ldw >= K, "lda/ldw smaller than K");
+  DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
+  DLM_REQUIRE(2LL * M * lda < (1LL << 31) && 2LL * N * ldw < (1LL << 31), "X or W larger than 2 GiB");
+  DLM_REQUIRE(act >= DLM_ACT_NONE && act <= DLM_ACT_GELU, "unknown act");
+  DLM_REQUIRE(ldy >= N && (!R || ldr >= N), "ldy / ldr smaller than N");
+  hipStream_t s = (hipStream_t)stream;
+  RowDesc ad{(const f16*)X, lda, M, K, (unsigned)((size_t)M * lda * 2)};
+  RowDesc bd{(const f16*)W, ldw, N, K, (unsigned)((size_t)N * ldw * 2)};
+  EpiArgs ep = make_epi(Y, ldy, bias, R, ldr, M, N, alpha, beta, act);
+  ep.gn_stats = (float2*)gn_stats;
+  ep.gn_hw = tokens;
+  ep.gn_chunks = (tokens + kGnChunk - 1) / kGnChunk;
+  t_gn_written = false;
+  const int st = launch_gemm(ad, bd, ep, M, N, s);
+  if (st != DLM_OK || t_gn_written) return st;
+  return gn_chunk_stats(Y, ldy, M / tokens, tokens, N, (float2*)gn_stats, s);
 }
 
 int dlm_linear_vt_fp16(const void* X, int lda, const void* W, int ldw, const void* bias, void* Y,
@@ -2492,6 +2588,12 @@ int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* a, void* stream) {
               "operand larger than 2 GiB");
   DLM_REQUIRE((C0 % BK == 0 && a->C0a % BK == 0) || a->C0b == 0,
               "channel concatenation needs 64-aligned channel counts");
+  if (a->gn_stats) {
+    DLM_REQUIRE(!a->out_nchw && !a->out_f32, "gn_stats needs fp16 channels-last output");
+    DLM_REQUIRE(a->Cout % 8 == 0 && a->ldy % 8 == 0, "gn_stats needs Cout and ldy multiples of 8");
+    DLM_REQUIRE(dlm_aligned16(a->out) && dlm_aligned16(a->gn_stats), "gn_stats: out and gn_stats 16-byte aligned");
+    DLM_REQUIRE((long long)Ho * Wo <= 65536, "gn_stats covers at most 65536 output pixels per sample");
+  }
   return conv_nhwc_impl(a, ConvGeom{a->stride, a->stride, a->pad, a->pad, 1, 1}, (hipStream_t)stream);
 }
 

@@ -285,6 +285,13 @@ int dlm_unet_set_ln_fold(void* handle, int on) {
   });
 }
 
+int dlm_unet_set_gn_fold(void* handle, int on) {
+  return guarded([&] {
+    if (!handle) throw std::invalid_argument("NULL handle");
+    static_cast<UNet*>(handle)->set_gn_fold(on != 0);
+  });
+}
+
 int dlm_unet_graphs_captured(void* handle, size_t* count) {
   return guarded([&] {
     if (!handle || !count) throw std::invalid_argument("NULL argument");

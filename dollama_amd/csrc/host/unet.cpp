@@ -404,6 +404,11 @@ void UNet::set_ln_fold(int mask) {
   ln_fold_ = mask;
 }
 
+void UNet::set_gn_fold(bool on) {
+  if (on != gn_fold_) clear_graphs();
+  gn_fold_ = on;
+}
+
 void UNet::place_copy(const std::string& name, void* dst, size_t n) {
   Placement pl;
   pl.kind = Placement::kCopy;
@@ -716,9 +721,24 @@ void UNet::stage(const char* name, const void* p, size_t n, int C, void* stream)
   hook_(name, p, n, C, hook_user_);
 }
 
+// A GroupNorm workspace whose statistics a producer fills (null where the
+// chunk statistics do not apply: more than 65536 pixels per sample, or the
+// fold is off).
+static void* gn_stats_ws(DeviceArenaScope& sc, int B, int C, int HW, bool on = true) {
+  if (!on || HW > 65536) return nullptr;
+  return sc.alloc_bytes(dlm_group_norm_nhwc_workspace_bytes(B, C, HW));
+}
+
 void UNet::gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, const void* b,
-              void* out, int B, int HW, float eps, bool silu, void* stream) {
+              void* out, int B, int HW, float eps, bool silu, void* stream, const void* prestats) {
   const int C = Ca + Cb;
+  if (prestats) {
+    if (xb) throw std::logic_error("UNet::gn: producer statistics cover one source");
+    LAUNCH(kGroupNorm, 0.0, 4.0 * B * HW * C,
+           dlm_group_norm_nhwc_prestats_fp16(xa, C, g, b, out, C, B, HW, C, cfg_.groups, eps,
+                                             silu ? 1 : 0, const_cast<void*>(prestats), stream));
+    return;
+  }
   DeviceArenaScope sc(DeviceArenaId::UNet);
   void* ws = sc.alloc_bytes(dlm_group_norm_nhwc_workspace_bytes(B, C, HW));
   LAUNCH(kGroupNorm, 0.0, 4.0 * B * HW * C,
@@ -727,7 +747,7 @@ void UNet::gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, con
 }
 
 void UNet::conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, void* out, int Co,
-                 int B, int H, int W, int stride, bool up, void* stream, int flop_cin) {
+                 int B, int H, int W, int stride, bool up, void* stream, int flop_cin, void* gn_stats) {
   dlm_conv_nhwc_args a{};
   a.src0a = x;
   a.C0a = C;
@@ -749,6 +769,7 @@ void UNet::conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, vo
   a.bias = c.b;
   a.out = out;
   a.ldy = Co;
+  a.gn_stats = gn_stats;
   const int Ho = (up ? 2 * H : (H + 2 - 3) / stride + 1), Wo = (up ? 2 * W : (W + 2 - 3) / stride + 1);
   const double cin = flop_cin > 0 ? flop_cin : (double)(C + Cb);
   LAUNCH(kConv, 2.0 * B * Ho * Wo * Co * 9.0 * cin,
@@ -757,15 +778,18 @@ void UNet::conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, vo
 }
 
 void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out,
-                  int B, int H, int W, const void* tproj, void* stream) {
+                  int B, int H, int W, const void* tproj, void* stream, const void* in_stats,
+                  void* out_stats) {
   const int HW = H * W;
   const int Ci = Ca + Cb, Co = r.Co;
   if (Ci != r.Ci) throw std::logic_error("UNet::resnet: input channel mismatch");
   DeviceArenaScope sc(DeviceArenaId::UNet);
   void* h = sc.alloc<uint16_t>((size_t)B * HW * std::max(Ci, Co));
   void* h2 = sc.alloc<uint16_t>((size_t)B * HW * Co);
+  // conv1 writes norm2's statistics
+  void* st2 = gn_stats_ws(sc, B, Co, HW, gn_fold_);
   // norm1 + SiLU over concat(xa, xb)
-  gn(xa, Ca, xb, Cb, r.n1g, r.n1b, h, B, HW, 1e-5f, true, stream);
+  gn(xa, Ca, xb, Cb, r.n1g, r.n1b, h, B, HW, 1e-5f, true, stream, in_stats);
   // conv1 + bias + time_emb_proj(silu(temb)) per (n, c)
   {
     dlm_conv_nhwc_args a{};
@@ -787,12 +811,13 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
     a.tbias_ld = tproj_total_;
     a.out = h2;
     a.ldy = Co;
+    a.gn_stats = st2;
     LAUNCH(kConv, 2.0 * B * HW * Co * 9.0 * Ci,
            2.0 * ((double)B * HW * Ci + (double)Co * 9.0 * Ci + (double)B * HW * Co),
            dlm_conv2d_nhwc_fp16(&a, stream));
   }
   // norm2 + SiLU
-  gn(h2, Co, nullptr, 0, r.n2g, r.n2b, h, B, HW, 1e-5f, true, stream);
+  gn(h2, Co, nullptr, 0, r.n2g, r.n2b, h, B, HW, 1e-5f, true, stream, st2);
   // conv2 + bias + (fused 1x1 shortcut over the block input | identity residual)
   {
     dlm_conv_nhwc_args a{};
@@ -812,6 +837,7 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
     a.bias = r.c2b;
     a.out = out;
     a.ldy = Co;
+    a.gn_stats = out_stats;
     if (r.shortcut) {
       a.src1a = xa;
       a.C1a = Ca;
@@ -937,7 +963,8 @@ void UNet::tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int
                            DLM_ACT_NONE, stream));
 }
 
-void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream) {
+void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream,
+               const void* in_stats, void* out_stats) {
   const int C = t.C;
   const int M = B * HW;
   DeviceArenaScope sc(DeviceArenaId::UNet);
@@ -952,16 +979,23 @@ void UNet::t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_
   void* o = sc.alloc<uint16_t>((size_t)M * C);
   void* f = sc.alloc<uint16_t>((size_t)M * 4 * C);
 
-  gn(x, C, nullptr, 0, t.ng, t.nb, g, B, HW, 1e-6f, false, stream);
+  gn(x, C, nullptr, 0, t.ng, t.nb, g, B, HW, 1e-6f, false, stream, in_stats);
   LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, false),
          dlm_linear_fp16(g, C, t.pin_w, C, t.pin_b, nullptr, 0, h, C, M, C, C, 1.0f, 0.0f,
                            DLM_ACT_NONE, stream));
   const TScratch ts{n, qkv, vt, vt_ld, o, f};
   for (const Block& k : t.blocks) tblock(k, C, h, ts, B, HW, kv, k.kv_off, kv_total_ / 2, ctx_len, stream);
-  // proj_out + residual (the block input), written back in place
-  LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
-         dlm_linear_fp16(h, C, t.pout_w, C, t.pout_b, x, C, x, C, M, C, C, 1.0f, 1.0f,
+  // proj_out + residual (the block input), written back in place (with the
+  // next GroupNorm's statistics when out_stats is given)
+  if (out_stats) {
+    LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
+           dlm_linear_gn_stats_fp16(h, C, t.pout_w, C, t.pout_b, x, C, x, C, M, C, C, 1.0f, 1.0f,
+                                    DLM_ACT_NONE, HW, out_stats, stream));
+  } else {
+    LAUNCH(kLinear, 2.0 * M * C * C, lin_bytes(M, C, C, C, true),
+           dlm_linear_fp16(h, C, t.pout_w, C, t.pout_b, x, C, x, C, M, C, C, 1.0f, 1.0f,
                            DLM_ACT_NONE, stream));
+  }
 }
 
 static std::string with_dot(const std::string& p) {
@@ -1132,59 +1166,79 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
   // ---- conv_in (latent NCHW -> channels-last, zero-padded to 64 channels)
   void* xin = P((size_t)B * HW0 * kConvInPad);
   LAUNCH(kOther, 0.0, 0.0, dlm_nchw_to_nhwc_fp16(latent, xin, B, c.in_channels, HW0, kConvInPad, stream));
+  // GroupNorm statistics written by the conv that produces a GroupNorm's
+  // single-source input (conv1 -> norm2 inside each resnet; here: conv_in,
+  // the downsamplers and resnet outputs that feed a GroupNorm directly)
+  auto S = [&](int C, int HWs) { return gn_stats_ws(persist, B, C, HWs, gn_fold_); };
   void* cur = P((size_t)B * HW0 * C0);
-  conv3(conv_in_, xin, kConvInPad, nullptr, 0, cur, C0, B, H, W, 1, false, stream, c.in_channels);
+  void* cur_st = S(C0, HW0);
+  conv3(conv_in_, xin, kConvInPad, nullptr, 0, cur, C0, B, H, W, 1, false, stream, c.in_channels, cur_st);
   stage("conv_in_out", cur, (size_t)B * HW0 * C0, C0, stream);
   skips.push_back({cur, C0});
 
   // ---- down_blocks.0
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW0 * C0);
-    resnet(res_[ri++], cur, C0, nullptr, 0, o, B, H, W, tproj, stream);
+    void* o_st = r == 0 ? S(C0, HW0) : nullptr;  // the second resnet's output feeds the downsampler
+    resnet(res_[ri++], cur, C0, nullptr, 0, o, B, H, W, tproj, stream, cur_st, o_st);
     skips.push_back({o, C0});
     cur = o;
+    cur_st = o_st;
   }
   {
     void* d = P((size_t)B * HW1 * C0);
-    conv3(down0_, cur, C0, nullptr, 0, d, C0, B, H, W, 2, false, stream);
+    cur_st = S(C0, HW1);
+    conv3(down0_, cur, C0, nullptr, 0, d, C0, B, H, W, 2, false, stream, -1, cur_st);
     skips.push_back({d, C0});
     cur = d;
   }
   stage("down_block_0_out", cur, (size_t)B * HW1 * C0, C0, stream);
-  // ---- down_blocks.1
+  // ---- down_blocks.1 (the first transformer's proj_out writes the second
+  // resnet's norm1 statistics; the second's output feeds the downsampler)
   int curC = C0;
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW1 * C1);
-    resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H1, W1, tproj, stream);
-    t2d(t2d_[ai++], o, B, HW1, ckv, ctx_len, stream);
+    void* o_st = S(C1, HW1);
+    void* t_st = r == 0 ? S(C1, HW1) : nullptr;
+    resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H1, W1, tproj, stream, cur_st, o_st);
+    t2d(t2d_[ai++], o, B, HW1, ckv, ctx_len, stream, o_st, t_st);
     skips.push_back({o, C1});
     cur = o;
+    cur_st = t_st;
     curC = C1;
   }
   {
     void* d = P((size_t)B * HW2 * C1);
-    conv3(down1_, cur, C1, nullptr, 0, d, C1, B, H1, W1, 2, false, stream);
+    cur_st = S(C1, HW2);
+    conv3(down1_, cur, C1, nullptr, 0, d, C1, B, H1, W1, 2, false, stream, -1, cur_st);
     skips.push_back({d, C1});
     cur = d;
   }
   stage("down_block_1_out", cur, (size_t)B * HW2 * C1, C1, stream);
   // ---- down_blocks.2
+  // (both transformers' proj_out write the next resnet's norm1 statistics:
+  // the second resnet's, then the mid block's first)
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW2 * C2);
-    resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H2, W2, tproj, stream);
-    t2d(t2d_[ai++], o, B, HW2, ckv, ctx_len, stream);
+    void* o_st = S(C2, HW2);
+    void* t_st = S(C2, HW2);
+    resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H2, W2, tproj, stream, cur_st, o_st);
+    t2d(t2d_[ai++], o, B, HW2, ckv, ctx_len, stream, o_st, t_st);
     skips.push_back({o, C2});
     cur = o;
+    cur_st = t_st;
     curC = C2;
   }
   stage("down_block_2_out", cur, (size_t)B * HW2 * C2, C2, stream);
   // ---- mid_block
   {
     void* m0 = P((size_t)B * HW2 * C2);
-    resnet(res_[ri++], cur, C2, nullptr, 0, m0, B, H2, W2, tproj, stream);
-    t2d(t2d_[ai++], m0, B, HW2, ckv, ctx_len, stream);
+    void* m0_st = S(C2, HW2);
+    void* t_st = S(C2, HW2);
+    resnet(res_[ri++], cur, C2, nullptr, 0, m0, B, H2, W2, tproj, stream, cur_st, m0_st);
+    t2d(t2d_[ai++], m0, B, HW2, ckv, ctx_len, stream, m0_st, t_st);
     void* m1 = P((size_t)B * HW2 * C2);
-    resnet(res_[ri++], m0, C2, nullptr, 0, m1, B, H2, W2, tproj, stream);
+    resnet(res_[ri++], m0, C2, nullptr, 0, m1, B, H2, W2, tproj, stream, t_st);
     cur = m1;
   }
   stage("mid_block_out", cur, (size_t)B * HW2 * C2, C2, stream);
@@ -1198,15 +1252,19 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
       const auto sk = skips.back();
       skips.pop_back();
       void* o = P((size_t)B * HWu * C);
-      resnet(res_[ri++], cur, curC, sk.first, sk.second, o, B, Hh, Ww, tproj, stream);
-      if (depth[u] > 0) t2d(t2d_[ai++], o, B, HWu, ckv, ctx_len, stream);
+      // a transformer's GroupNorm, or conv_norm_out after the last resnet
+      void* o_st = depth[u] > 0 || (u == 2 && r == 2) ? S(C, HWu) : nullptr;
+      resnet(res_[ri++], cur, curC, sk.first, sk.second, o, B, Hh, Ww, tproj, stream, nullptr, o_st);
+      if (depth[u] > 0) t2d(t2d_[ai++], o, B, HWu, ckv, ctx_len, stream, o_st);
       cur = o;
+      cur_st = depth[u] > 0 ? nullptr : o_st;  // the transformer rewrote o in place
       curC = C;
     }
     if (u < 2) {
       void* up = P((size_t)B * 4 * HWu * C);
       conv3(u == 0 ? up0_ : up1_, cur, C, nullptr, 0, up, C, B, Hh, Ww, 1, true, stream);
       cur = up;
+      cur_st = nullptr;
     }
     static const char* names[3] = {"up_block_0_out", "up_block_1_out", "up_block_2_out"};
     const int HWo = u < 2 ? 4 * HWu : HWu;
@@ -1218,7 +1276,7 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
   {
     DeviceArenaScope sc(DeviceArenaId::UNet);
     void* g = sc.alloc<uint16_t>((size_t)B * HW0 * C0);
-    gn(cur, C0, nullptr, 0, norm_out_g_, norm_out_b_, g, B, HW0, 1e-5f, true, stream);
+    gn(cur, C0, nullptr, 0, norm_out_g_, norm_out_b_, g, B, HW0, 1e-5f, true, stream, cur_st);
     dlm_conv_nhwc_args a{};
     a.src0a = g;
     a.C0a = C0;

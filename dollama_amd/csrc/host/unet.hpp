@@ -125,6 +125,11 @@ class UNet {
   // Q and GEGLU linears (on by default) or run as separate launches
   void set_ln_fold(int mask);
   int ln_fold() const { return ln_fold_; }
+  // GroupNorm statistics written by the producing conv's epilogue (on by
+  // default); off, every GroupNorm runs its own statistics pass.  Same bits
+  // either way.
+  void set_gn_fold(bool on);
+  bool gn_fold() const { return gn_fold_; }
   size_t graphs_captured() const { return graphs_.size(); }
 
   // Per-launch timing with device events, grouped by kernel class.  While
@@ -225,6 +230,7 @@ class UNet {
   // LayerNorms folded into their consuming linears: bit 0 norm1 -> QKV,
   // bit 1 norm2 -> cross-attention Q (both by default: step 23.07 -> 22.76 ms)
   int ln_fold_ = 3;
+  bool gn_fold_ = true;
   LnFold make_fold(const void* w, const void* g, const void* b, const void* bias, int N, int K,
                    const std::vector<std::string>& deps, void* stream);
   void refold(const LnFold& f, void* stream);
@@ -234,15 +240,19 @@ class UNet {
   std::set<std::vector<uint64_t>> seen_;
 
   // forward pieces
+  // in_stats: GroupNorm chunk statistics of xa (no xb) already written by
+  // its producer, or null; out_stats: where conv2 writes those of out, or null
   void resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out, int B,
-              int H, int W, const void* tproj, void* stream);
+              int H, int W, const void* tproj, void* stream, const void* in_stats = nullptr,
+              void* out_stats = nullptr);
   // every block's cross-attention K ([B*ctx, sumC]) and V^T ([B, sumC, ld])
   struct CrossKV {
     void* k;
     void* vt;
     int ld;
   };
-  void t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream);
+  void t2d(const T2D& t, void* x, int B, int HW, const CrossKV& kv, int ctx_len, void* stream,
+           const void* in_stats = nullptr, void* out_stats = nullptr);
   // one BasicTransformerBlock over the residual stream h [B*HW, C]; this
   // block's context K rows start at row kv_off of kv.k (row stride kv_stride)
   // and its V^T rows at row kv_off of kv.vt (kv_stride rows per sample)
@@ -253,10 +263,13 @@ class UNet {
   };
   void tblock(const Block& k, int C, void* h, const TScratch& ts, int B, int HW, const CrossKV& kv,
               int kv_off, int kv_stride, int ctx_len, void* stream);
+  // prestats: a GroupNorm workspace whose chunk statistics of xa (no xb)
+  // its producer wrote (dlm_conv_nhwc_args::gn_stats), or null
   void gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, const void* b, void* out,
-          int B, int HW, float eps, bool silu, void* stream);
+          int B, int HW, float eps, bool silu, void* stream, const void* prestats = nullptr);
   void conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, void* out, int Co, int B,
-             int H, int W, int stride, bool up, void* stream, int flop_cin = -1);
+             int H, int W, int stride, bool up, void* stream, int flop_cin = -1,
+             void* gn_stats = nullptr);
   void stage(const char* name, const void* p, size_t n, int C, void* stream);
 
   UNetConfig cfg_;

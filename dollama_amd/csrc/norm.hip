@@ -15,9 +15,17 @@
 // per-channel scale/shift, and a vectorised apply (+SiLU) pass.
 // Deterministic: fixed reduction order.
 //
+// fp16 inputs of up to 65536 pixels per sample (every UNet GroupNorm) use the
+// per-channel chunk statistics of common.hpp (64-pixel chunks, [N][chunks][C])
+// instead of the per-group partials: a GEMM / conv epilogue can write those
+// for its own output (dlm_conv_nhwc_args::gn_stats), and then the GroupNorm
+// runs from them (dlm_group_norm_nhwc_prestats_fp16) with no statistics pass.
+// The statistics pass computes the same values bit for bit.
+//
 // LayerNorm replaces launch_layer_norm (src/kernels/layernorm.cu:78-126):
 // one wave per row, the row held in registers, exact two-pass mean/variance.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -48,9 +56,23 @@ static GnPlan gn_plan(int N, int C, int HW) {
   return p;
 }
 
+// Per-channel chunk statistics (the form a producer's epilogue can write):
+// fp16 inputs with at most this many pixels per sample.
+constexpr int kGnChanMaxHW = 65536;
+static inline int gn_chan_chunks(int HW) { return (HW + kGnChunk - 1) / kGnChunk; }
+
 static size_t gn_workspace_bytes(int N, int C, int HW) {
   const GnPlan p = gn_plan(N, C, HW);
-  return (size_t)N * p.chunks * C * sizeof(float2) + (size_t)N * C * sizeof(float2) + 256;
+  const size_t legacy = (size_t)N * p.chunks * C * sizeof(float2);
+  const size_t chan = HW <= kGnChanMaxHW ? (size_t)N * gn_chan_chunks(HW) * C * sizeof(float2) : 0;
+  return std::max(legacy, chan) + (size_t)N * C * sizeof(float2) + 256;
+}
+// scale/shift follow the statistics, 16-byte aligned
+static float2* gn_ss_of(void* ws, int N, int C, int HW) {
+  const GnPlan p = gn_plan(N, C, HW);
+  const size_t legacy = (size_t)N * p.chunks * C * sizeof(float2);
+  const size_t chan = HW <= kGnChanMaxHW ? (size_t)N * gn_chan_chunks(HW) * C * sizeof(float2) : 0;
+  return (float2*)(((uintptr_t)ws + std::max(legacy, chan) + 15) & ~(uintptr_t)15);
 }
 
 __device__ __forceinline__ void load8(const f16* p, float (&v)[8]) {
@@ -122,8 +144,10 @@ __global__ void gn_partial_kernel(const T* __restrict__ a, int Ca, int lda,
       s2[i] += d * d;
     }
   }
+  // LDS entries channel-interleaved (channel s*8+i at i*S+s), so the lanes of
+  // one store or load touch consecutive 8-byte words
 #pragma unroll
-  for (int i = 0; i < 8; ++i) red[r * C + c + i] = make_float2(s1[i], s2[i]);
+  for (int i = 0; i < 8; ++i) red[r * C + i * S + s] = make_float2(s1[i], s2[i]);
   __syncthreads();
   const float cnt = (float)(p1 - p0);
   float2 mc[8];
@@ -132,7 +156,7 @@ __global__ void gn_partial_kernel(const T* __restrict__ a, int Ca, int lda,
     for (int i = 0; i < 8; ++i) {
       float t1 = 0.0f, t2 = 0.0f;
       for (int rr = 0; rr < R; ++rr) {
-        const float2 q = red[rr * C + c + i];
+        const float2 q = red[rr * C + i * S + s];
         t1 += q.x;
         t2 += q.y;
       }
@@ -143,17 +167,18 @@ __global__ void gn_partial_kernel(const T* __restrict__ a, int Ca, int lda,
   __syncthreads();
   if (r == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) red[c + i] = mc[i];
+    for (int i = 0; i < 8; ++i) red[i * S + s] = mc[i];
   }
   __syncthreads();
   const int cpg = C / G;
+  auto chan = [&](int ch) { return red[(ch & 7) * S + (ch >> 3)]; };
   for (int g = tid; g < G; g += blockDim.x) {
     float mean = 0.0f;
-    for (int ci = 0; ci < cpg; ++ci) mean += red[g * cpg + ci].x;
+    for (int ci = 0; ci < cpg; ++ci) mean += chan(g * cpg + ci).x;
     mean /= (float)cpg;
     float m2 = 0.0f;
     for (int ci = 0; ci < cpg; ++ci) {
-      const float2 q = red[g * cpg + ci];
+      const float2 q = chan(g * cpg + ci);
       const float d = q.x - mean;
       m2 += q.y + cnt * d * d;
     }
@@ -220,6 +245,115 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
   }
 }
 
+// Per-channel chunk statistics of fp16 [N, HW, C] (+ concatenated second
+// source): one thread per (chunk, 8-channel vector), the chunk's rows in
+// ascending order, eight rows' loads in flight.
+__global__ void __launch_bounds__(256)
+gn_chan_stats_kernel(const f16* __restrict__ a, int Ca, int lda, const f16* __restrict__ b, int ldb,
+                     int HW, int C, int S, int chunks, float2* __restrict__ stats) {
+  const int n = blockIdx.y;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = idx / S, s = idx - k * S;
+  if (k >= chunks) return;
+  const int c = s * 8;
+  const f16* src;
+  int ld;
+  if (c < Ca) {
+    src = a + (size_t)n * HW * lda + c;
+    ld = lda;
+  } else {
+    src = b + (size_t)n * HW * ldb + (c - Ca);
+    ld = ldb;
+  }
+  const int p0 = k * kGnChunk, p1 = min(HW, p0 + kGnChunk);
+  float shift[8], s1[8], s2[8];
+  load8(src + (size_t)p0 * ld, shift);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s1[i] = s2[i] = 0.0f;
+  int p = p0;
+  for (; p + 8 <= p1; p += 8) {
+    float v[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) load8(src + (size_t)(p + u) * ld, v[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) gn_stat_add(v[u][i], shift[i], s1[i], s2[i]);
+  }
+  for (; p < p1; ++p) {
+    float v[8];
+    load8(src + (size_t)p * ld, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) gn_stat_add(v[i], shift[i], s1[i], s2[i]);
+  }
+  float4* dst = reinterpret_cast<float4*>(stats + ((size_t)n * chunks + k) * C + c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float2 e0 = gn_stat_finish(s1[2 * i], s2[2 * i], shift[2 * i], p1 - p0);
+    const float2 e1 = gn_stat_finish(s1[2 * i + 1], s2[2 * i + 1], shift[2 * i + 1], p1 - p0);
+    dst[i] = make_float4(e0.x, e0.y, e1.x, e1.y);
+  }
+}
+
+// Merge of the per-channel chunk statistics of one (n, group), one 256-thread
+// block each, in fp64 by the same two-pass decomposition as
+// gn_finalize_kernel; entry j = (chunk j / cpg, channel j % cpg) of the
+// group; per-thread sums in order, then the xor butterfly and the four
+// waves' results added in wave order, so every thread holds the same,
+// launch-invariant result.
+__device__ __forceinline__ double gn_block_sum(double v, double* red) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // red free (an earlier sum's readers are done)
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__global__ void __launch_bounds__(256)
+gn_chan_finalize_kernel(const float2* __restrict__ stats, int HW, int C, int G, int chunks,
+                        const f16* __restrict__ gamma, const f16* __restrict__ beta, float eps,
+                        float2* __restrict__ ss) {
+  __shared__ double red[4];
+  const int n = blockIdx.x / G, g = blockIdx.x % G;
+  const int cpg = C / G;
+  const int total = chunks * cpg;
+  const float2* base = stats + (size_t)n * chunks * C + g * cpg;
+  auto entry = [&](int j, double& nb) {
+    const int k = j / cpg, ci = j - k * cpg;
+    nb = (double)(min(HW, (k + 1) * kGnChunk) - k * kGnChunk);
+    return base[(size_t)k * C + ci];
+  };
+  double cnt = 0.0, s1 = 0.0;
+  for (int j = threadIdx.x; j < total; j += 256) {
+    double nb;
+    const float2 q = entry(j, nb);
+    cnt += nb;
+    s1 = fma(nb, (double)q.x, s1);
+  }
+  cnt = gn_block_sum(cnt, red);
+  s1 = gn_block_sum(s1, red);
+  const double mean = cnt > 0.0 ? s1 / cnt : 0.0;
+  double m2 = 0.0;
+  for (int j = threadIdx.x; j < total; j += 256) {
+    double nb;
+    const float2 q = entry(j, nb);
+    const double d = (double)q.x - mean;
+    m2 += (double)q.y + nb * d * d;
+  }
+  m2 = gn_block_sum(m2, red);
+  const double var = cnt > 0.0 ? fmax(m2 / cnt, 0.0) : 0.0;
+  const float rstd = (float)(1.0 / sqrt(var + (double)eps));
+  for (int ci = threadIdx.x; ci < cpg; ci += 256) {
+    const int c = g * cpg + ci;
+    const float gm = gamma ? (float)gamma[c] : 1.0f;
+    const float bt = beta ? (float)beta[c] : 0.0f;
+    const float scale = gm * rstd;
+    ss[(size_t)n * C + c] = make_float2(scale, bt - (float)mean * scale);
+  }
+}
+
 // Apply: same blocks as the statistics pass (one chunk of one sample's
 // pixels, S * R threads).  A thread owns one 8-channel vector for the whole
 // chunk: its source (concat half), scale and shift are fixed, so they are
@@ -277,41 +411,72 @@ __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
   }
 }
 
+static int gn_chan_stats_launch(const f16* a, int C_a, int ld_a, const f16* b, int ld_b, int N,
+                                int HW, int C, float2* stats, hipStream_t s) {
+  const int S = C / 8, chunks = gn_chan_chunks(HW);
+  DLM_LAUNCH("gn_chan_stats_kernel", gn_chan_stats_kernel, dim3((chunks * S + 255) / 256, N), dim3(256), 0, s, a,
+             C_a, ld_a, b, ld_b, HW, C, S, chunks, stats);
+  DLM_LAUNCH_CHECK();
+  return DLM_OK;
+}
+
+int gn_chunk_stats(const void* x, int ld, int N, int HW, int C, float2* stats, hipStream_t s) {
+  return gn_chan_stats_launch((const f16*)x, C, ld, (const f16*)x, ld, N, HW, C, stats, s);
+}
+
+// prestats: the per-channel chunk statistics are already at the start of ws
 template <typename T>
 static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
                              const void* gamma, const void* beta, void* out, int ld_out, int N,
-                             int HW, int C, int G, float eps, int silu, void* ws, hipStream_t s) {
+                             int HW, int C, int G, float eps, int silu, void* ws, hipStream_t s,
+                             bool prestats = false) {
   const GnPlan p = gn_plan(N, C, HW);
   float2* partial = (float2*)ws;
-  float2* ss = partial + (size_t)N * p.chunks * G;
-  ss = (float2*)(((uintptr_t)ss + 15) & ~(uintptr_t)15);
+  float2* ss = gn_ss_of(ws, N, C, HW);
   const T* a = (const T*)in_a;
   const T* b = in_b ? (const T*)in_b : a;
   const long long total_vec = (long long)N * HW * (C / 8);
   if (total_vec >= (1LL << 31) || (long long)N * HW * std::max(ld_a, ld_out) >= (1LL << 31))
     return fail(DLM_ERR_UNSUPPORTED, "group_norm: tensor too large for 32-bit indexing");
-  const size_t red_bytes = (size_t)p.R * C * sizeof(float2);
-  if (red_bytes > 160 * 1024)
-    return fail(DLM_ERR_UNSUPPORTED, "group_norm: channel count too large for one block");
-  DLM_LAUNCH("gn_partial_kernel", gn_partial_kernel<T>, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
-                     ld_a, b, ld_b, HW, C, G, p.chunk, p.chunks, p.S, p.R, partial);
-  DLM_LAUNCH_CHECK();
-  DLM_LAUNCH("gn_finalize_kernel", gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
-                     p.chunks, (const f16*)gamma, (const f16*)beta, eps, ss);
-  DLM_LAUNCH_CHECK();
-  DLM_LAUNCH("gn_partial_kernel+gn_finalize_kernel+gn_apply_kernel", gn_apply_kernel<T>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a,
-                     b, ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss, silu);
+  if (std::is_same<T, f16>::value && HW <= kGnChanMaxHW) {
+    if (!prestats) {
+      const int st = gn_chan_stats_launch((const f16*)a, C_a, ld_a, (const f16*)b, ld_b, N, HW, C, partial, s);
+      if (st != DLM_OK) return st;
+    }
+    DLM_LAUNCH("gn_chan_finalize_kernel", gn_chan_finalize_kernel, dim3(N * G), dim3(256), 0, s, partial, HW, C,
+               G, gn_chan_chunks(HW), (const f16*)gamma, (const f16*)beta, eps, ss);
+    DLM_LAUNCH_CHECK();
+  } else {
+    if (prestats) return fail(DLM_ERR_UNSUPPORTED, "group_norm: chunk statistics need fp16 input of <= 65536 pixels");
+    const size_t red_bytes = (size_t)p.R * C * sizeof(float2);
+    if (red_bytes > 160 * 1024)
+      return fail(DLM_ERR_UNSUPPORTED, "group_norm: channel count too large for one block");
+    DLM_LAUNCH("gn_partial_kernel", gn_partial_kernel<T>, dim3(p.chunks, N), dim3(p.threads), red_bytes, s, a, C_a,
+               ld_a, b, ld_b, HW, C, G, p.chunk, p.chunks, p.S, p.R, partial);
+    DLM_LAUNCH_CHECK();
+    DLM_LAUNCH("gn_finalize_kernel", gn_finalize_kernel, dim3(N * G), dim3(64), 0, s, partial, HW, C, G, p.chunk,
+               p.chunks, (const f16*)gamma, (const f16*)beta, eps, ss);
+    DLM_LAUNCH_CHECK();
+  }
+  // the entry's label: the kernels of the whole GroupNorm
+  const char* label = !(std::is_same<T, f16>::value && HW <= kGnChanMaxHW)
+                          ? "gn_partial_kernel+gn_finalize_kernel+gn_apply_kernel"
+                          : (prestats ? "gn_chan_finalize_kernel+gn_apply_kernel"
+                                      : "gn_chan_stats_kernel+gn_chan_finalize_kernel+gn_apply_kernel");
+  DLM_LAUNCH(label, gn_apply_kernel<T>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b, ld_b,
+             (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss, silu);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
 
 int group_norm_nhwc(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
                     const void* gamma, const void* beta, void* out, int ld_out, int N, int HW,
-                    int C, int G, float eps, int silu, void* ws, hipStream_t s, bool in_f32 = false) {
+                    int C, int G, float eps, int silu, void* ws, hipStream_t s, bool in_f32 = false,
+                    bool prestats = false) {
   return in_f32 ? group_norm_nhwc_t<float>(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N,
-                                           HW, C, G, eps, silu, ws, s)
+                                           HW, C, G, eps, silu, ws, s, prestats)
                 : group_norm_nhwc_t<f16>(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N,
-                                         HW, C, G, eps, silu, ws, s);
+                                         HW, C, G, eps, silu, ws, s, prestats);
 }
 
 // ---------------------------------------------------------------------------
@@ -461,6 +626,31 @@ int dlm_group_norm_nhwc_fp16(const void* in_a, int C_a, int ld_a, const void* in
   DLM_REQUIRE(dlm_aligned16(workspace), "workspace must be 16-byte aligned");
   return group_norm_nhwc(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N, HW, C,
                          num_groups, eps, fuse_silu, workspace, (hipStream_t)stream);
+}
+
+int dlm_group_norm_nhwc_prestats_fp16(const void* in, int ld_in, const void* gamma, const void* beta,
+                                      void* out, int ld_out, int N, int HW, int C, int num_groups,
+                                      float eps, int fuse_silu, void* workspace, void* stream) {
+  if (N <= 0 || HW <= 0 || C <= 0 || num_groups <= 0) return DLM_OK;
+  DLM_REQUIRE(in && out && workspace, "NULL pointer");
+  DLM_REQUIRE(C % num_groups == 0, "C must be divisible by num_groups");
+  DLM_REQUIRE(C % 8 == 0, "C must be a multiple of 8");
+  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 65536 pixels per sample");
+  DLM_REQUIRE(ld_in % 8 == 0 && ld_in >= C && ld_out % 8 == 0 && ld_out >= C, "bad row strides");
+  DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(out) && dlm_aligned16(workspace),
+              "buffers must be 16-byte aligned");
+  return group_norm_nhwc(in, C, ld_in, nullptr, 0, gamma, beta, out, ld_out, N, HW, C, num_groups, eps,
+                         fuse_silu, workspace, (hipStream_t)stream, false, true);
+}
+
+int dlm_group_norm_chunk_stats_fp16(const void* in, int ld_in, int N, int HW, int C, void* workspace,
+                                    void* stream) {
+  if (N <= 0 || HW <= 0 || C <= 0) return DLM_OK;
+  DLM_REQUIRE(in && workspace, "NULL pointer");
+  DLM_REQUIRE(C % 8 == 0 && ld_in % 8 == 0 && ld_in >= C, "C and ld_in must be multiples of 8, ld_in >= C");
+  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 65536 pixels per sample");
+  DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(workspace), "buffers must be 16-byte aligned");
+  return gn_chunk_stats(in, ld_in, N, HW, C, (float2*)workspace, (hipStream_t)stream);
 }
 
 int dlm_group_norm_nhwc_f32in(const float* in, int ld_in, const void* gamma, const void* beta,

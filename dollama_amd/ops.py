@@ -259,9 +259,12 @@ def launch_timestep_embedding(d_out, timestep, dim, max_period=10000.0):
 # Channels-last fused helpers (native forms)
 # ---------------------------------------------------------------------------
 def linear(x: torch.Tensor, w: torch.Tensor, bias=None, residual=None, act=ACT_NONE,
-           out=None, alpha=1.0, beta=1.0) -> torch.Tensor:
+           out=None, alpha=1.0, beta=1.0, gn_stats: Optional[torch.Tensor] = None,
+           tokens: int = 0) -> torch.Tensor:
     """y = act(alpha * x @ w.T + bias) + beta * residual.  x [M,K], w [N,K].
-    For ACT_GEGLU, w/bias must be packed with ``pack_geglu`` and y has N/2 columns."""
+    For ACT_GEGLU, w/bias must be packed with ``pack_geglu`` and y has N/2 columns.
+    gn_stats: a GroupNorm workspace that receives y's chunk statistics, y
+    holding M / tokens samples of `tokens` rows."""
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K:
@@ -274,6 +277,13 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias=None, residual=None, act=ACT_N
     _need(bias, N, "bias", optional=True)
     _need(residual, M * ncols, "residual", optional=True)
     _need(out, M * ncols, "out")
+    if gn_stats is not None:
+        if tokens <= 0 or M % tokens:
+            raise ValueError("gn_stats needs M = samples x tokens")
+        _need(gn_stats, group_norm_workspace_bytes(M // tokens, N, tokens), "gn_stats", dtype=torch.uint8)
+        call("dlm_linear_gn_stats_fp16", _p(x), K, _p(w), K, _p(bias), _p(residual), ncols, _p(out), ncols,
+             M, N, K, float(alpha), float(beta), int(act), int(tokens), _p(gn_stats), stream_handle())
+        return out
     call("dlm_linear_fp16", _p(x), K, _p(w), K, _p(bias), _p(residual), ncols, _p(out), ncols,
          M, N, K, float(alpha), float(beta), int(act), stream_handle())
     return out
@@ -439,11 +449,14 @@ def conv2d_nhwc(x: torch.Tensor, w_packed: torch.Tensor, *, KH: int, KW: int, st
                 bias=None, tbias=None, residual=None, x_b: Optional[torch.Tensor] = None,
                 upsample=False, shortcut: Optional[torch.Tensor] = None,
                 shortcut_b: Optional[torch.Tensor] = None, act=ACT_NONE, out=None,
-                out_nchw=False, cout: Optional[int] = None, out_f32=False) -> torch.Tensor:
+                out_nchw=False, cout: Optional[int] = None, out_f32=False,
+                gn_stats: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Channels-last implicit-GEMM conv.  x [N,H,W,Ca] (+ x_b [N,H,W,Cb] concatenated),
     optional fused 1x1 shortcut over concat(shortcut, shortcut_b), weight from
     ``pack_conv_weight`` (segment-1 columns appended).  The residual may be
-    fp16 or fp32; out_f32 gives an fp32 output."""
+    fp16 or fp32; out_f32 gives an fp32 output.  gn_stats: a GroupNorm
+    workspace (``group_norm_workspace``) that receives the output's chunk
+    statistics, for ``group_norm_nhwc_prestats``."""
     N, H, W, Ca = x.shape
     Cb = 0 if x_b is None else x_b.shape[3]
     C1a = 0 if shortcut is None else shortcut.shape[3]
@@ -479,6 +492,9 @@ def conv2d_nhwc(x: torch.Tensor, w_packed: torch.Tensor, *, KH: int, KW: int, st
     a.residual, a.res_ld = _p(residual), Cout
     a.out, a.ldy, a.out_nchw, a.act = _p(out), Cout, int(out_nchw), int(act)
     a.out_f32, a.res_f32 = int(out_f32), int(res_f32)
+    if gn_stats is not None:
+        _need(gn_stats, group_norm_workspace_bytes(N, Cout, Ho * Wo), "gn_stats", dtype=torch.uint8)
+    a.gn_stats = _p(gn_stats)
     call("dlm_conv2d_nhwc_fp16", ctypes.byref(a), stream_handle())
     return out
 
@@ -513,6 +529,41 @@ def group_norm_nhwc(x: torch.Tensor, gamma, beta, groups: int, eps: float, silu:
         return out
     call("dlm_group_norm_nhwc_fp16", _p(x), Ca, Ca, _p(x_b), max(Cb, 8), _p(gamma), _p(beta),
          _p(out), C, N, HW, C, groups, float(eps), int(silu), _p(ws), stream_handle())
+    return out
+
+
+def group_norm_workspace_bytes(N: int, C: int, HW: int) -> int:
+    return int(_lib.hip_lib().dlm_group_norm_nhwc_workspace_bytes(N, C, HW))
+
+
+def group_norm_workspace(N: int, C: int, HW: int, device) -> torch.Tensor:
+    """A GroupNorm workspace; its first bytes hold the chunk statistics."""
+    return torch.empty(group_norm_workspace_bytes(N, C, HW), dtype=torch.uint8, device=device)
+
+
+def group_norm_chunk_stats(x: torch.Tensor, ws: torch.Tensor) -> torch.Tensor:
+    """Chunk statistics of fp16 [N,H,W,C] into the workspace ws (returned)."""
+    N, H, W, C = x.shape
+    _need(x, N * H * W * C, "x")
+    _need(ws, group_norm_workspace_bytes(N, C, H * W), "ws", dtype=torch.uint8)
+    call("dlm_group_norm_chunk_stats_fp16", _p(x), C, N, H * W, C, _p(ws), stream_handle())
+    return ws
+
+
+def group_norm_nhwc_prestats(x: torch.Tensor, gamma, beta, groups: int, eps: float, silu: bool,
+                             ws: torch.Tensor, out=None) -> torch.Tensor:
+    """GroupNorm of fp16 [N,H,W,C] whose chunk statistics are already in ws."""
+    N, H, W, C = x.shape
+    HW = H * W
+    _need(x, N * HW * C, "x")
+    _need(gamma, C, "gamma", optional=True)
+    _need(beta, C, "beta", optional=True)
+    _need(ws, group_norm_workspace_bytes(N, C, HW), "ws", dtype=torch.uint8)
+    if out is None:
+        out = torch.empty(N, H, W, C, dtype=torch.float16, device=x.device)
+    _need(out, N * HW * C, "out")
+    call("dlm_group_norm_nhwc_prestats_fp16", _p(x), C, _p(gamma), _p(beta), _p(out), C, N, HW, C,
+         groups, float(eps), int(silu), _p(ws), stream_handle())
     return out
 
 

@@ -64,6 +64,7 @@ HOST_SIGNATURES = {
     "dlm_unet_set_profiling": (I, [P, I]),
     "dlm_unet_set_graphs": (I, [P, I]),
     "dlm_unet_set_ln_fold": (I, [P, I]),
+    "dlm_unet_set_gn_fold": (I, [P, I]),
     "dlm_unet_graphs_captured": (I, [P, POINTER(c_size_t)]),
     "dlm_unet_profile_report": (I, [P, POINTER(ctypes.c_double), P]),
     "dlm_euler_schedule": (I, [I, POINTER(ctypes.c_float), POINTER(ctypes.c_float)]),
@@ -334,6 +335,11 @@ class UNet:
         """Bit mask (0-3) of the LayerNorms folded into their consuming linears:
         bit 0 norm1 -> QKV, bit 1 norm2 -> cross-attention Q (default 3)."""
         _call("dlm_unet_set_ln_fold", self._h, int(mask))
+
+    def set_gn_fold(self, on: bool):
+        """GroupNorm statistics written by the producing convs (default on);
+        off, every GroupNorm runs its own statistics pass (same bits)."""
+        _call("dlm_unet_set_gn_fold", self._h, int(bool(on)))
 
     def set_graphs(self, on: bool):
         """HIP-graph replay of repeated forwards (needs a non-default torch stream)."""

@@ -243,6 +243,17 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
                     const void* R, int ldr, void* Y, int ldy, int M, int N, int K,
                     float alpha, float beta, int act, void* stream);
 
+/* dlm_linear_fp16 (act none/silu/gelu) that also writes the GroupNorm chunk
+ * statistics of Y, as dlm_conv_nhwc_args::gn_stats does: Y holds
+ * M / tokens samples of tokens rows (tokens <= 65536); gn_stats is a
+ * GroupNorm workspace of dlm_group_norm_nhwc_workspace_bytes(M / tokens, N,
+ * tokens) bytes for dlm_group_norm_nhwc_prestats_fp16.  N and ldy multiples
+ * of 8.  No counterpart in the reference (the transformer's proj_out feeding
+ * the next ResnetBlock2D's GroupNorm). */
+int dlm_linear_gn_stats_fp16(const void* X, int lda, const void* W, int ldw, const void* bias,
+                             const void* R, int ldr, void* Y, int ldy, int M, int N, int K, float alpha,
+                             float beta, int act, int tokens, void* gn_stats, void* stream);
+
 /* Linear with a transposed tail: Y = X W^T for columns [0, vt_col0) (row
  * stride ldy) and, for columns n >= vt_col0, the transpose per sample:
  * VT[(m / tokens) * (N - vt_col0) + n - vt_col0][m % tokens] with row stride
@@ -336,7 +347,14 @@ int dlm_nhwc_to_nchw_fp16(const void* in, void* out, int N, int C, int HW, int C
  * stride ldw.  Output channels-last with row
  * stride ldy, or NCHW when out_nchw = 1; fp32 output elements when
  * out_f32 = 1 and an fp32 residual when res_f32 = 1 (the VAE decoder's fp32
- * stages, src/kernels/vae_decode.cu:317-327; operands stay fp16). */
+ * stages, src/kernels/vae_decode.cu:317-327; operands stay fp16).
+ * gn_stats (may be NULL): the GroupNorm chunk statistics of the output are
+ * also written there, as the first bytes of a GroupNorm workspace
+ * (dlm_group_norm_nhwc_workspace_bytes(N, Cout, Ho*Wo)) that
+ * dlm_group_norm_nhwc_prestats_fp16 then normalises the output with, with no
+ * statistics pass; fp16 channels-last output, Cout and ldy multiples of 8,
+ * Ho*Wo <= 65536.  The values equal dlm_group_norm_chunk_stats_fp16's on the
+ * output bit for bit, whichever kernel the convolution runs. */
 typedef struct dlm_conv_nhwc_args {
   const void* src0a; const void* src0b; int C0a; int C0b; int ld0a; int ld0b;
   const void* src1a; const void* src1b; int C1a; int C1b; int ld1a; int ld1b;
@@ -347,6 +365,7 @@ typedef struct dlm_conv_nhwc_args {
   void* out; int ldy; int out_nchw; int act;
   int out_f32;  /* 1: out holds fp32 elements */
   int res_f32;  /* 1: residual holds fp32 elements */
+  void* gn_stats; /* GroupNorm chunk statistics of the output, or NULL */
 } dlm_conv_nhwc_args;
 int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* args, void* stream);
 
@@ -360,6 +379,24 @@ int dlm_group_norm_nhwc_fp16(const void* in_a, int C_a, int ld_a, const void* in
                              const void* gamma, const void* beta, void* out, int ld_out,
                              int N, int HW, int C, int num_groups, float eps, int fuse_silu,
                              void* workspace, void* stream);
+/* GroupNorm chunk statistics: per channel c of sample n, over the pixel rows
+ * [64k, min(64k + 64, HW)) of chunk k, shift = the chunk's first value,
+ * s1 = sum (x - shift), s2 = sum (x - shift)^2 (fp32, rows in order), stored
+ * as float2 (shift + s1/cnt, max(s2 - s1 * s1/cnt, 0)) at [n][k][c] from the
+ * start of a GroupNorm workspace.  fp16 input, HW <= 65536.  No counterpart
+ * in the reference: the statistics half of the GroupNorm, which producers
+ * write from their epilogues (dlm_conv_nhwc_args::gn_stats). */
+int dlm_group_norm_chunk_stats_fp16(const void* in, int ld_in, int N, int HW, int C, void* workspace,
+                                    void* stream);
+/* dlm_group_norm_nhwc_fp16 (one source, fp16, HW <= 65536) whose workspace
+ * already holds the input's chunk statistics (written by a producer with
+ * gn_stats, or by dlm_group_norm_chunk_stats_fp16): the merge and the apply
+ * pass only.  Same result as dlm_group_norm_nhwc_fp16 on that input, bit for
+ * bit.  No counterpart in the reference (its GroupNorm computes the
+ * statistics itself, src/kernels/groupnorm.cu:91-148). */
+int dlm_group_norm_nhwc_prestats_fp16(const void* in, int ld_in, const void* gamma, const void* beta,
+                                      void* out, int ld_out, int N, int HW, int C, int num_groups,
+                                      float eps, int fuse_silu, void* workspace, void* stream);
 /* Same GroupNorm(+SiLU) over fp32 channels-last input (one source), fp16
  * output: the VAE decoder's fp32 stages (reference launch_group_norm_f32,
  * src/kernels/vae_decode.cu:466-545). */

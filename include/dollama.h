@@ -145,6 +145,13 @@ int dlm_unet_graphs_captured(void* handle, size_t* count);
  * kept in step with LoRA patches and their removal. */
 int dlm_unet_set_ln_fold(void* handle, int mask);
 
+/* GroupNorm statistics from the producers (on = 1, the default): a conv
+ * whose output feeds a GroupNorm directly writes that GroupNorm's chunk
+ * statistics from its epilogue (dlm_conv_nhwc_args::gn_stats) and the
+ * GroupNorm runs no statistics pass; on = 0 runs the pass everywhere.  The
+ * output is the same bit for bit.  No counterpart in the reference. */
+int dlm_unet_set_gn_fold(void* handle, int on);
+
 /* Per-launch kernel timing (device events around every launch of a
  * forward).  Classes: 0 conv, 1 linear, 2 attention, 3 groupnorm,
  * 4 layernorm, 5 other.  report fills, per class, out[4*c + 0..3] =

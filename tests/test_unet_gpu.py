@@ -113,6 +113,40 @@ def test_unet_layernorm_fold_matches_unfolded(gpu):
     net.close()
 
 
+def test_unet_groupnorm_statistics_fold_is_bit_exact(gpu):
+    """GroupNorm statistics written by the producing convs' epilogues (the
+    default) give the same noise_pred, bit for bit, as a statistics pass in
+    every GroupNorm, eager and under graph replay, at a latent whose deepest
+    level (4x4) leaves a partial 64-pixel chunk."""
+    cfg = TINY
+    Wc = OR.random_weights(OR.TINY, seed=23)
+    net = U.UNet(cfg)
+    net.set_weights(_to_gpu(Wc))
+    net.prepare()
+    for H in (32, 16):
+        print(f"[case] tiny UNet GroupNorm statistics fold on/off, latent {H}x{H}", flush=True)
+        lat, ts, ehs, text, ids = _inputs(cfg, 2, H, H, 77, seed=24)
+        args = (lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
+        net.set_gn_fold(False)
+        ref = net.forward(*args).clone()
+        net.set_gn_fold(True)
+        on = net.forward(*args).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(on, ref), f"latent {H}: producer statistics change the output"
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        out = torch.empty_like(ref)
+        net.set_graphs(True)
+        for i in range(4):  # first sight, capture + launch, replays
+            out.zero_()
+            net.forward(*args, out=out)
+            s.synchronize()
+            assert torch.equal(out, ref), f"graph call {i} with producer statistics differs"
+        assert net.graphs_captured == 1
+        net.set_graphs(False)
+    net.close()
+
+
 def test_unet_profiled_forward_times_each_kernel(gpu):
     """Profiling attaches a device event pair to each call's kernels in their
     own dispatches (dlm_prof_arm): the profiled forward equals the plain eager
