@@ -96,3 +96,34 @@ def test_denoise_loop_with_graphs_equals_eager(gpu):
             assert torch.equal(a, b), f"denoise run {i} with graphs differs"
         assert net.graphs_captured == 1
     net.close()
+
+
+def test_split_k_conv_captured_on_a_fresh_stream(gpu):
+    """A conv whose heuristic picks split-K (2048 x 1280 x 11520: the
+    1280-channel level's 3x3 conv at B=2), captured on a stream that never
+    ran it eagerly: no workspace can be made under capture, so the captured
+    launch runs unsplit; the capture succeeds, every replay gives the same
+    bits, and they match the eager (split) result to fp32 summation order."""
+    from dollama_amd import ops
+    from tests._util import assert_close, randn, to_gpu
+    print("[case] split-K conv 2048x1280x11520 captured on a fresh stream", flush=True)
+    x = ops.nchw_to_nhwc(to_gpu(randn((2, 1280, 32, 32), 700)))
+    wp = ops.pack_conv_weight(to_gpu(randn((1280, 1280, 3, 3), 701, std=0.01)))
+    b = to_gpu(randn((1280,), 702, std=0.1))
+    eager = ops.conv2d_nhwc(x, wp, KH=3, KW=3, bias=b)
+    torch.cuda.synchronize()
+    y = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ops.conv2d_nhwc(x, wp, KH=3, KW=3, bias=b, out=y)
+    outs = []
+    for _ in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        outs.append(y.clone())
+    assert all(torch.equal(o, outs[0]) for o in outs), "replays differ"
+    assert_close(outs[0], eager.float().cpu(), "captured unsplit vs eager split-K", rel_tol=1e-3,
+                 cos_tol=0.999999)
