@@ -2299,7 +2299,7 @@ int dlm_linear_gn_stats_fp16(const void* X, int lda, const void* W, int ldw, con
   if (M <= 0 || N <= 0 || K <= 0) return DLM_OK;
   DLM_REQUIRE(gn_stats, "gn_stats is NULL (use dlm_linear_fp16)");
   DLM_REQUIRE(act != DLM_ACT_GEGLU, "gn_stats with a GEGLU output");
-  DLM_REQUIRE(tokens > 0 && M % tokens == 0 && tokens <= 65536, "M must be samples x tokens, tokens <= 65536");
+  DLM_REQUIRE(tokens > 0 && M % tokens == 0 && tokens <= 16384, "M must be samples x tokens, tokens <= 16384");
   DLM_REQUIRE(N % 8 == 0 && ldy % 8 == 0 && dlm_aligned16(Y) && dlm_aligned16(gn_stats),
               "gn_stats needs N and ldy multiples of 8 and 16-byte aligned Y / gn_stats");
   DLM_REQUIRE(X && W && Y, "NULL operand");
@@ -2592,7 +2592,7 @@ int dlm_conv2d_nhwc_fp16(const dlm_conv_nhwc_args* a, void* stream) {
     DLM_REQUIRE(!a->out_nchw && !a->out_f32, "gn_stats needs fp16 channels-last output");
     DLM_REQUIRE(a->Cout % 8 == 0 && a->ldy % 8 == 0, "gn_stats needs Cout and ldy multiples of 8");
     DLM_REQUIRE(dlm_aligned16(a->out) && dlm_aligned16(a->gn_stats), "gn_stats: out and gn_stats 16-byte aligned");
-    DLM_REQUIRE((long long)Ho * Wo <= 65536, "gn_stats covers at most 65536 output pixels per sample");
+    DLM_REQUIRE((long long)Ho * Wo <= 16384, "gn_stats covers at most 16384 output pixels per sample");
   }
   return conv_nhwc_impl(a, ConvGeom{a->stride, a->stride, a->pad, a->pad, 1, 1}, (hipStream_t)stream);
 }

@@ -722,10 +722,10 @@ void UNet::stage(const char* name, const void* p, size_t n, int C, void* stream)
 }
 
 // A GroupNorm workspace whose statistics a producer fills (null where the
-// chunk statistics do not apply: more than 65536 pixels per sample, or the
+// chunk statistics do not apply: more than 16384 pixels per sample, or the
 // fold is off).
 static void* gn_stats_ws(DeviceArenaScope& sc, int B, int C, int HW, bool on = true) {
-  if (!on || HW > 65536) return nullptr;
+  if (!on || HW > 16384) return nullptr;
   return sc.alloc_bytes(dlm_group_norm_nhwc_workspace_bytes(B, C, HW));
 }
 

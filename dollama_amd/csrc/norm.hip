@@ -15,7 +15,7 @@
 // per-channel scale/shift, and a vectorised apply (+SiLU) pass.
 // Deterministic: fixed reduction order.
 //
-// fp16 inputs of up to 65536 pixels per sample (every UNet GroupNorm) use the
+// fp16 inputs of up to 16384 pixels per sample (every UNet GroupNorm at 1024²) use the
 // per-channel chunk statistics of common.hpp (64-pixel chunks, [N][chunks][C])
 // instead of the per-group partials: a GEMM / conv epilogue can write those
 // for its own output (dlm_conv_nhwc_args::gn_stats), and then the GroupNorm
@@ -58,7 +58,7 @@ static GnPlan gn_plan(int N, int C, int HW) {
 
 // Per-channel chunk statistics (the form a producer's epilogue can write):
 // fp16 inputs with at most this many pixels per sample.
-constexpr int kGnChanMaxHW = 65536;
+constexpr int kGnChanMaxHW = 16384;
 static inline int gn_chan_chunks(int HW) { return (HW + kGnChunk - 1) / kGnChunk; }
 
 static size_t gn_workspace_bytes(int N, int C, int HW) {
@@ -447,7 +447,7 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
                G, gn_chan_chunks(HW), (const f16*)gamma, (const f16*)beta, eps, ss);
     DLM_LAUNCH_CHECK();
   } else {
-    if (prestats) return fail(DLM_ERR_UNSUPPORTED, "group_norm: chunk statistics need fp16 input of <= 65536 pixels");
+    if (prestats) return fail(DLM_ERR_UNSUPPORTED, "group_norm: chunk statistics need fp16 input of <= 16384 pixels");
     const size_t red_bytes = (size_t)p.R * C * sizeof(float2);
     if (red_bytes > 160 * 1024)
       return fail(DLM_ERR_UNSUPPORTED, "group_norm: channel count too large for one block");
@@ -635,7 +635,7 @@ int dlm_group_norm_nhwc_prestats_fp16(const void* in, int ld_in, const void* gam
   DLM_REQUIRE(in && out && workspace, "NULL pointer");
   DLM_REQUIRE(C % num_groups == 0, "C must be divisible by num_groups");
   DLM_REQUIRE(C % 8 == 0, "C must be a multiple of 8");
-  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 65536 pixels per sample");
+  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 16384 pixels per sample");
   DLM_REQUIRE(ld_in % 8 == 0 && ld_in >= C && ld_out % 8 == 0 && ld_out >= C, "bad row strides");
   DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(out) && dlm_aligned16(workspace),
               "buffers must be 16-byte aligned");
@@ -648,7 +648,7 @@ int dlm_group_norm_chunk_stats_fp16(const void* in, int ld_in, int N, int HW, in
   if (N <= 0 || HW <= 0 || C <= 0) return DLM_OK;
   DLM_REQUIRE(in && workspace, "NULL pointer");
   DLM_REQUIRE(C % 8 == 0 && ld_in % 8 == 0 && ld_in >= C, "C and ld_in must be multiples of 8, ld_in >= C");
-  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 65536 pixels per sample");
+  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 16384 pixels per sample");
   DLM_REQUIRE(dlm_aligned16(in) && dlm_aligned16(workspace), "buffers must be 16-byte aligned");
   return gn_chunk_stats(in, ld_in, N, HW, C, (float2*)workspace, (hipStream_t)stream);
 }

@@ -245,7 +245,7 @@ int dlm_linear_fp16(const void* X, int lda, const void* W, int ldw, const void* 
 
 /* dlm_linear_fp16 (act none/silu/gelu) that also writes the GroupNorm chunk
  * statistics of Y, as dlm_conv_nhwc_args::gn_stats does: Y holds
- * M / tokens samples of tokens rows (tokens <= 65536); gn_stats is a
+ * M / tokens samples of tokens rows (tokens <= 16384); gn_stats is a
  * GroupNorm workspace of dlm_group_norm_nhwc_workspace_bytes(M / tokens, N,
  * tokens) bytes for dlm_group_norm_nhwc_prestats_fp16.  N and ldy multiples
  * of 8.  No counterpart in the reference (the transformer's proj_out feeding
@@ -353,7 +353,7 @@ int dlm_nhwc_to_nchw_fp16(const void* in, void* out, int N, int C, int HW, int C
  * (dlm_group_norm_nhwc_workspace_bytes(N, Cout, Ho*Wo)) that
  * dlm_group_norm_nhwc_prestats_fp16 then normalises the output with, with no
  * statistics pass; fp16 channels-last output, Cout and ldy multiples of 8,
- * Ho*Wo <= 65536.  The values equal dlm_group_norm_chunk_stats_fp16's on the
+ * Ho*Wo <= 16384.  The values equal dlm_group_norm_chunk_stats_fp16's on the
  * output bit for bit, whichever kernel the convolution runs. */
 typedef struct dlm_conv_nhwc_args {
   const void* src0a; const void* src0b; int C0a; int C0b; int ld0a; int ld0b;
@@ -383,12 +383,12 @@ int dlm_group_norm_nhwc_fp16(const void* in_a, int C_a, int ld_a, const void* in
  * [64k, min(64k + 64, HW)) of chunk k, shift = the chunk's first value,
  * s1 = sum (x - shift), s2 = sum (x - shift)^2 (fp32, rows in order), stored
  * as float2 (shift + s1/cnt, max(s2 - s1 * s1/cnt, 0)) at [n][k][c] from the
- * start of a GroupNorm workspace.  fp16 input, HW <= 65536.  No counterpart
+ * start of a GroupNorm workspace.  fp16 input, HW <= 16384.  No counterpart
  * in the reference: the statistics half of the GroupNorm, which producers
  * write from their epilogues (dlm_conv_nhwc_args::gn_stats). */
 int dlm_group_norm_chunk_stats_fp16(const void* in, int ld_in, int N, int HW, int C, void* workspace,
                                     void* stream);
-/* dlm_group_norm_nhwc_fp16 (one source, fp16, HW <= 65536) whose workspace
+/* dlm_group_norm_nhwc_fp16 (one source, fp16, HW <= 16384) whose workspace
  * already holds the input's chunk statistics (written by a producer with
  * gn_stats, or by dlm_group_norm_chunk_stats_fp16): the merge and the apply
  * pass only.  Same result as dlm_group_norm_nhwc_fp16 on that input, bit for

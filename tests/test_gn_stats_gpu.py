@@ -107,7 +107,7 @@ def test_linear_gn_stats_equal_stats_pass(gpu, tile):
                                               (1, 1280, 32, 32, -3.0, 2.0), (3, 64, 9, 7, 0.5, 1.5)])
 def test_group_norm_chunk_statistics_vs_oracle(gpu, N, C, H, W, mean, std):
     """GroupNorm(+SiLU) over the chunk statistics (the path of every fp16
-    GroupNorm of up to 65536 pixels) against the float64 oracle on the same
+    GroupNorm of up to 16384 pixels) against the float64 oracle on the same
     fp16 values, at the UNet's three level shapes, a mean 80x the standard
     deviation, and a pixel count that leaves a partial last chunk; the
     prestats form from the statistics pass gives the same bits."""
