@@ -689,13 +689,15 @@ struct ConvDma {
     const bool s1 = k0 >= K0;
     const int cs = k0 - K0;  // segment-1 K index of the slice
     const bool isa0 = cur_c < C0a, isa1 = cs < C1a;
-    const f16* src = s1 ? pick(isa1, s1a, s1b) : pick(isa0, s0a, s0b);
-    const unsigned bytes = s1 ? pick(isa1, bytes1a, bytes1b) : pick(isa0, bytes0a, bytes0b);
+    // arithmetic selects throughout: a ternary between members lets the
+    // compiler select their addresses instead, which moves them to scratch
+    const f16* src = pick(s1, pick(isa1, s1a, s1b), pick(isa0, s0a, s0b));
+    const unsigned bytes = pick(s1, pick(isa1, bytes1a, bytes1b), pick(isa0, bytes0a, bytes0b));
     rs = dma_rsrc(src, bytes);
-    ld = rfl(s1 ? pick(isa1, ld1a, ld1b) : pick(isa0, ld0a, ld0b));
-    cbase = rfl(s1 ? pick(isa1, cs, cs - C1a) : pick(isa0, cur_c, cur_c - C0a));
-    kh = rfl(s1 ? cs : cur_kh * dil_h);  // segment 0: tap offset in input rows
-    kw = rfl(s1 ? 0 : cur_kw * dil_w);
+    ld = rfl(pick(s1, pick(isa1, ld1a, ld1b), pick(isa0, ld0a, ld0b)));
+    cbase = rfl(pick(s1, pick(isa1, cs, cs - C1a), pick(isa0, cur_c, cur_c - C0a)));
+    kh = rfl(pick(s1, cs, cur_kh * dil_h));  // segment 0: tap offset in input rows
+    kw = rfl(pick(s1, 0, cur_kw * dil_w));
     seg = rfl(s1 ? 1 : 0);
   }
   // Both segment offsets are always computed and chosen with arithmetic
