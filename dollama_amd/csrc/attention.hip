@@ -539,13 +539,15 @@ flash_vt_pipe_kernel(FlashVtParams p) {
   auto last = [&](f32x16 (&sc)[2]) {
     const int kt = nkt - 1;
     if (kt * FA_TK + FA_TK > p.Sk) {
+      // element e of key block kb holds tile key fa_perm(kb*32 + mfma_row(e, lane))
+      // = 8g + kb*32 + 16*(e>>3) + 4*((e>>2)&1) + (e&3): one lane-dependent
+      // limit against per-element constants
+      const int lim = p.Sk - kt * FA_TK - 8 * g;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kt * FA_TK + fa_perm(kb * 32 + mfma_row(e, lane));
-          if (key >= p.Sk) sc[kb][e] = -INFINITY;
-        }
+        for (int e = 0; e < 16; ++e)
+          if (kb * 32 + 16 * (e >> 3) + 4 * ((e >> 2) & 1) + (e & 3) >= lim) sc[kb][e] = -INFINITY;
     }
     f16x8 vf[8];
     vread(smem + cur * FA_STAGE, vf);
