@@ -296,7 +296,7 @@ __device__ __forceinline__ float fa_sum_halves(float x) {
 // K/V fragments between two blocks: the softmax is VALU work that other
 // waves' MFMAs hide): the scores of tile kt+1 (MFMA) are issued before the
 // softmax of tile kt (VALU), so each wave's own MFMAs run in the shadow of
-// its exp / max / convert work.  The barrier that publishes tile kt+1 also
+// its exp / convert / row-sum work.  The barrier that publishes tile kt+1 also
 // proves every wave is done with tile kt-1, whose buffer then receives tile
 // kt+2: one tile of DMA latency hidden, three buffers.  Full tiles carry no
 // masking code; the rescale is a real (rare) branch; the row sum is taken
@@ -414,10 +414,10 @@ flash_vt_pipe_kernel(FlashVtParams p) {
 
   // Running state, in log2 units: the scores of a tile arrive as s - m with m
   // the lane's current base (negm = -m broadcast is every score chain's
-  // accumulator start).  The base moves only when a tile's max exceeds it by
-  // more than 8 (a rare, wave-uniform branch), so P <= 2^8 stays exact in
-  // fp16.  The next tile's scores are issued before this tile's softmax; when
-  // that softmax moves the base it re-bases them too.
+  // accumulator start).  The base moves only when a tile's P would overflow
+  // fp16 (a rare, wave-uniform branch; see softmax below).  The next tile's
+  // scores are issued before this tile's softmax; when that softmax moves the
+  // base it re-bases them too.
   float l_run = 0.0f;
   f32x16 negm;
   f32x16 o[2];
@@ -437,24 +437,41 @@ flash_vt_pipe_kernel(FlashVtParams p) {
       d8[(e & 7) + 1] = hr[1];
     }
   };
+  // the lane's sum of its 32 fp16 P values (two terms per dot2, fp32
+  // accumulate), in four chains so the check below waits on four dot2
+  auto row_sum = [&](const f16x8 (&pf)[4]) {
+    float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; t += 2)
+        l[j] = __builtin_amdgcn_fdot2(f16x2{pf[j][t], pf[j][t + 1]}, f16x2{(f16)1.0f, (f16)1.0f}, l[j], false);
+    return (l[0] + l[1]) + (l[2] + l[3]);
+  };
   // softmax of one tile's (shifted) scores sv into fp16 P; sn, when given,
   // holds the next tile's scores, already issued against the current base.
-  // The exponentials of key block 0 are taken before the growth check (held
-  // there by an empty asm that reads them), so they run under the next
-  // tile's score MFMAs; the rare growth branch redoes them.
+  // No per-tile max: p = 2^s is exact to fp16 precision up to 65504, so the
+  // base has to move only when some p of the tile overflowed, which the row
+  // sum the denominator needs anyway shows (it is then not finite; 32 finite
+  // fp16 values sum to at most 2.1e6).  The first tile (base 0) also moves it
+  // down when its row sum is below 2^-8, so the row's largest p is a normal
+  // fp16 number and a row whose scores all lie far below 0 cannot underflow
+  // every p.  The rare branch takes the tile's max, re-bases the running
+  // state, this tile and the already issued next tile, and redoes the
+  // exponentials.
   auto softmax = [&](f32x16 (&sv)[2], f16x8 (&pf)[4], f32x16* sn, bool first) {
-    float mt = sv[0][0];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sv[kb][e]);
     exp_block(sv[0], pf[0], pf[1]);
-    asm volatile("" ::"v"(pf[0]), "v"(pf[1]));
-    mt = fa_max_halves(mt);
-    // the first tile (base 0) also re-bases downwards, so a row whose scores
-    // are all far below 0 cannot underflow every p
-    if (__builtin_amdgcn_ballot_w64(mt > 8.0f || (first && mt < -8.0f)) != 0) {
+    exp_block(sv[1], pf[2], pf[3]);
+    float lsum = row_sum(pf);
+    const bool low = first && fa_sum_halves(lsum) < (1.0f / 256.0f);
+    if (__builtin_amdgcn_ballot_w64(!(lsum <= 3.0e6f) || low) != 0) {
       asm volatile("" ::: "memory");  // a real branch: never evaluated speculatively
+      float mt = sv[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sv[kb][e]);
+      mt = fa_max_halves(mt);
       const float d = first ? mt : fmaxf(mt, 0.0f);
       const float alpha = __builtin_amdgcn_exp2f(-d);
       l_run *= alpha;
@@ -475,14 +492,9 @@ flash_vt_pipe_kernel(FlashVtParams p) {
           for (int e = 0; e < 16; ++e) sn[kb][e] -= d;
       }
       exp_block(sv[0], pf[0], pf[1]);
+      exp_block(sv[1], pf[2], pf[3]);
+      lsum = row_sum(pf);
     }
-    exp_block(sv[1], pf[2], pf[3]);
-    float lsum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int t = 0; t < 8; t += 2)
-        lsum = __builtin_amdgcn_fdot2(f16x2{pf[j][t], pf[j][t + 1]}, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
     l_run += lsum;
   };
   // O^T += V^T P^T over four 16-key steps (step j: tile keys 16j + 8g + [0, 8))
@@ -559,7 +571,7 @@ flash_vt_pipe_kernel(FlashVtParams p) {
   // loop-carried copy of the next tile's 32 scores is needed
   f32x16 sa[2], sb[2];
   // the base starts at 0: tile 0's softmax moves it to that tile's max when
-  // the max lies outside [-8, 8]
+  // a p overflows or the row's sum is below 2^-8
 #pragma unroll
   for (int e = 0; e < 16; ++e) negm[e] = 0.0f;
   scores(smem, sa, negm);
