@@ -311,39 +311,53 @@ __device__ __forceinline__ double gn_block_sum(double v, double* red) {
   return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
+// A (sample, group) of up to kGnFinStage entries (every UNet GroupNorm:
+// at most 256 chunks x 30 channels) is first copied into LDS, every load in
+// flight at once; the two passes then read LDS instead of making one global
+// round trip per loop iteration each.  Larger groups read global memory in
+// both passes.  Same sums in the same order either way.
+constexpr int kGnFinStage = 8192;
 __global__ void __launch_bounds__(256)
 gn_chan_finalize_kernel(const float2* __restrict__ stats, int HW, int C, int G, int chunks,
                         const f16* __restrict__ gamma, const f16* __restrict__ beta, float eps,
                         float2* __restrict__ ss) {
+  __shared__ float2 ent[kGnFinStage];
   __shared__ double red[4];
   const int n = blockIdx.x / G, g = blockIdx.x % G;
   const int cpg = C / G;
   const int total = chunks * cpg;
   const float2* base = stats + (size_t)n * chunks * C + g * cpg;
-  auto entry = [&](int j, double& nb) {
-    const int k = j / cpg, ci = j - k * cpg;
-    nb = (double)(min(HW, (k + 1) * kGnChunk) - k * kGnChunk);
-    return base[(size_t)k * C + ci];
-  };
-  double cnt = 0.0, s1 = 0.0;
-  for (int j = threadIdx.x; j < total; j += 256) {
-    double nb;
-    const float2 q = entry(j, nb);
-    cnt += nb;
-    s1 = fma(nb, (double)q.x, s1);
+  const bool staged = total <= kGnFinStage;
+  if (staged) {
+#pragma unroll 8
+    for (int j = threadIdx.x; j < total; j += 256) {
+      const int k = j / cpg;
+      ent[j] = base[(size_t)k * C + (j - k * cpg)];
+    }
+    __syncthreads();
   }
-  cnt = gn_block_sum(cnt, red);
+  auto entry = [&](int j) -> float2 {
+    if (staged) return ent[j];
+    const int k = j / cpg;
+    return base[(size_t)k * C + (j - k * cpg)];
+  };
+  // pixels in entry j's chunk: 64, except in a partial last chunk
+  const int last0 = (chunks - 1) * cpg;
+  const double nlast = (double)(HW - (chunks - 1) * kGnChunk);
+  auto count = [&](int j) { return j >= last0 ? nlast : (double)kGnChunk; };
+  const double cnt = (double)HW * cpg;
+  double s1 = 0.0;
+  for (int j = threadIdx.x; j < total; j += 256) s1 = fma(count(j), (double)entry(j).x, s1);
   s1 = gn_block_sum(s1, red);
-  const double mean = cnt > 0.0 ? s1 / cnt : 0.0;
+  const double mean = s1 / cnt;
   double m2 = 0.0;
   for (int j = threadIdx.x; j < total; j += 256) {
-    double nb;
-    const float2 q = entry(j, nb);
+    const float2 q = entry(j);
     const double d = (double)q.x - mean;
-    m2 += (double)q.y + nb * d * d;
+    m2 += (double)q.y + count(j) * d * d;
   }
   m2 = gn_block_sum(m2, red);
-  const double var = cnt > 0.0 ? fmax(m2 / cnt, 0.0) : 0.0;
+  const double var = fmax(m2 / cnt, 0.0);
   const float rstd = (float)(1.0 / sqrt(var + (double)eps));
   for (int ci = threadIdx.x; ci < cpg; ci += 256) {
     const int c = g * cpg + ci;
