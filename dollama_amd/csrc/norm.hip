@@ -373,11 +373,11 @@ gn_chan_finalize_kernel(const float2* __restrict__ stats, int HW, int C, int G, 
 // chunk: its source (concat half), scale and shift are fixed, so they are
 // resolved once and stay in registers, and the loop keeps four pixel rows in
 // flight per thread.
-template <typename T>
+template <typename T, bool SILU>
 __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
                                 const T* __restrict__ b, int ldb, f16* __restrict__ out,
                                 int ldo, int HW, int C, int S, int R, int chunk,
-                                const float2* __restrict__ ss, int silu) {
+                                const float2* __restrict__ ss) {
   const int n = blockIdx.y;
   const int r = threadIdx.x / S, s = threadIdx.x - r * S;
   const int c = s * 8;
@@ -416,7 +416,7 @@ __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float t = x[u][i] * sc[i] + sh[i];
-          if (silu) t = silu_f(t);
+          if constexpr (SILU) t = silu_f(t);
           y[i] = (f16)t;
         }
         *reinterpret_cast<f16x8*>(dst + (size_t)(p + u * R) * ldo) = y;
@@ -477,8 +477,12 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
                           ? "gn_partial_kernel+gn_finalize_kernel+gn_apply_kernel"
                           : (prestats ? "gn_chan_finalize_kernel+gn_apply_kernel"
                                       : "gn_chan_stats_kernel+gn_chan_finalize_kernel+gn_apply_kernel");
-  DLM_LAUNCH(label, gn_apply_kernel<T>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b, ld_b,
-             (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss, silu);
+  if (silu)
+    DLM_LAUNCH(label, gn_apply_kernel<T, true>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b, ld_b,
+               (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss);
+  else
+    DLM_LAUNCH(label, gn_apply_kernel<T, false>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b, ld_b,
+               (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss);
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
