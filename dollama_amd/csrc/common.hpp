@@ -13,6 +13,7 @@
 
 #include <string>
 #include <tuple>
+#include <type_traits>
 #include <utility>
 
 #include "../../include/dlm.h"
@@ -83,16 +84,62 @@ __device__ __forceinline__ float gelu_erf_fast(float x) {
   return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
 }
 
-// Wave-wide reductions (wave64) through the cross-lane permute network.
-__device__ __forceinline__ float wave_sum(float v) {
+// Wave-wide reductions (wave64) without LDS round trips: two DPP quad
+// permutations (lane ^ 1, lane ^ 2), the half-row and row mirrors (lane i with
+// 7 - i, then 15 - i: the other quad, then the other half-row), then the
+// row-pair and half-wave swaps of gfx950 (v_permlane16_swap,
+// v_permlane32_swap).  Each step adds the same two operands on both partners,
+// so every lane ends with the same value.  Needs all 64 lanes active.
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u32(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+  constexpr int W = sizeof(T) / 4;
+  auto step_dpp = [&](auto ctrl) {
+    unsigned w[W];
+    __builtin_memcpy(w, &v, sizeof(T));
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int i = 0; i < W; ++i) w[i] = dpp_u32<decltype(ctrl)::value>(w[i]);
+    T o;
+    __builtin_memcpy(&o, w, sizeof(T));
+    v = op(v, o);
+  };
+  step_dpp(std::integral_constant<int, kDppXor1>{});
+  step_dpp(std::integral_constant<int, kDppXor2>{});
+  step_dpp(std::integral_constant<int, kDppHalfMirror>{});
+  step_dpp(std::integral_constant<int, kDppMirror>{});
+  auto step_swap = [&](auto sw) {
+    unsigned w[W], a[W], b[W];
+    __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const auto s = sw(w[i]);
+      a[i] = s[0];
+      b[i] = s[1];
+    }
+    T x, y;
+    __builtin_memcpy(&x, a, sizeof(T));
+    __builtin_memcpy(&y, b, sizeof(T));
+    v = op(x, y);
+  };
+  step_swap([](unsigned u) { return __builtin_amdgcn_permlane16_swap(u, u, false, false); });
+  step_swap([](unsigned u) { return __builtin_amdgcn_permlane32_swap(u, u, false, false); });
   return v;
 }
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, [](float a, float b) { return a + b; });
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  return wave_reduce(v, [](double a, double b) { return a + b; });
 }
 
 // GroupNorm chunk statistics, one definition for every producer (the

@@ -201,7 +201,7 @@ __device__ __forceinline__ void chan_merge(double& n, double& mean, double& m2, 
 //   mean = sum(n_b m_b) / sum(n_b),  M2 = sum(M2_b + n_b (m_b - mean)^2),
 // which needs no division per chunk (a pairwise Chan merge needs one), then
 // emit per-channel scale = gamma*rstd and shift = beta - mean*scale.  Each
-// lane sums its chunks in order and the xor butterfly adds identical operand
+// lane sums its chunks in order and the wave reduction adds identical operand
 // pairs on both partners, so every lane ends with the same, launch-invariant
 // result.
 __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, int C, int G,
@@ -219,11 +219,8 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
     cnt += nb;
     s1 = fma(nb, (double)q.x, s1);
   }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    cnt += __shfl_xor(cnt, o, 64);
-    s1 += __shfl_xor(s1, o, 64);
-  }
+  cnt = wave_sum_f64(cnt);
+  s1 = wave_sum_f64(s1);
   const double mean = cnt > 0.0 ? s1 / cnt : 0.0;
   double m2 = 0.0;
   for (int chn = lane; chn < chunks; chn += 64) {
@@ -232,8 +229,7 @@ __global__ void gn_finalize_kernel(const float2* __restrict__ partial, int HW, i
     const double d = (double)q.x - mean;
     m2 += (double)q.y + nb * d * d;
   }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) m2 += __shfl_xor(m2, o, 64);
+  m2 = wave_sum_f64(m2);
   const double var = cnt > 0.0 ? fmax(m2 / cnt, 0.0) : 0.0;
   const float rstd = (float)(1.0 / sqrt(var + (double)eps));
   for (int ci = lane; ci < cpg; ci += 64) {
@@ -298,12 +294,11 @@ gn_chan_stats_kernel(const f16* __restrict__ a, int Ca, int lda, const f16* __re
 // Merge of the per-channel chunk statistics of one (n, group), one 256-thread
 // block each, in fp64 by the same two-pass decomposition as
 // gn_finalize_kernel; entry j = (chunk j / cpg, channel j % cpg) of the
-// group; per-thread sums in order, then the xor butterfly and the four
-// waves' results added in wave order, so every thread holds the same,
-// launch-invariant result.
+// group; per-thread sums in order, then the wave reduction (the same value
+// in every lane) and the four waves' results added in wave order, so every
+// thread holds the same, launch-invariant result.
 __device__ __forceinline__ double gn_block_sum(double v, double* red) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  v = wave_sum_f64(v);
   const int wave = threadIdx.x >> 6;
   __syncthreads();  // red free (an earlier sum's readers are done)
   if ((threadIdx.x & 63) == 0) red[wave] = v;
