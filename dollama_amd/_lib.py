@@ -131,6 +131,7 @@ HIP_SIGNATURES = {
     "dlm_linear_f32out_fp16": (I, [P, I, P, I, P, P, I, P, I, I, I, I, F, F, I, P]),
     "dlm_group_norm_nhwc_f32in": (I, [P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
     "dlm_group_norm_nhwc_prestats_fp16": (I, [P, I, P, P, P, I, I, I, I, I, F, I, P, P]),
+    "dlm_group_norm_nhwc_prestats2_fp16": (I, [P, I, I, P, I, P, P, P, P, P, I, I, I, I, I, F, I, P, P]),
     "dlm_group_norm_chunk_stats_fp16": (I, [P, I, I, I, I, P, P]),
     "dlm_cast_f32_to_f16": (I, [P, P, LL, F, P]),
     "dlm_scale_fp16": (I, [P, LL, F, P]),

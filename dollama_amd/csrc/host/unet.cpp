@@ -730,10 +730,19 @@ static void* gn_stats_ws(DeviceArenaScope& sc, int B, int C, int HW, bool on = t
 }
 
 void UNet::gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, const void* b,
-              void* out, int B, int HW, float eps, bool silu, void* stream, const void* prestats) {
+              void* out, int B, int HW, float eps, bool silu, void* stream, const void* prestats,
+              const void* prestats_b) {
   const int C = Ca + Cb;
+  if (xb && prestats && prestats_b) {  // concat(xa, xb), each source's producer statistics
+    DeviceArenaScope sc(DeviceArenaId::UNet);
+    void* ws = sc.alloc_bytes(dlm_group_norm_nhwc_workspace_bytes(B, C, HW));
+    LAUNCH(kGroupNorm, 0.0, 4.0 * B * HW * C,
+           dlm_group_norm_nhwc_prestats2_fp16(xa, Ca, Ca, xb, Cb, prestats, prestats_b, g, b, out, C, B, HW, C,
+                                              cfg_.groups, eps, silu ? 1 : 0, ws, stream));
+    return;
+  }
+  if (xb) prestats = nullptr;  // one source's statistics do not cover the concatenation
   if (prestats) {
-    if (xb) throw std::logic_error("UNet::gn: producer statistics cover one source");
     LAUNCH(kGroupNorm, 0.0, 4.0 * B * HW * C,
            dlm_group_norm_nhwc_prestats_fp16(xa, C, g, b, out, C, B, HW, C, cfg_.groups, eps,
                                              silu ? 1 : 0, const_cast<void*>(prestats), stream));
@@ -779,7 +788,7 @@ void UNet::conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, vo
 
 void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out,
                   int B, int H, int W, const void* tproj, void* stream, const void* in_stats,
-                  void* out_stats) {
+                  void* out_stats, const void* in_stats_b) {
   const int HW = H * W;
   const int Ci = Ca + Cb, Co = r.Co;
   if (Ci != r.Ci) throw std::logic_error("UNet::resnet: input channel mismatch");
@@ -789,7 +798,7 @@ void UNet::resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int C
   // conv1 writes norm2's statistics
   void* st2 = gn_stats_ws(sc, B, Co, HW, gn_fold_);
   // norm1 + SiLU over concat(xa, xb)
-  gn(xa, Ca, xb, Cb, r.n1g, r.n1b, h, B, HW, 1e-5f, true, stream, in_stats);
+  gn(xa, Ca, xb, Cb, r.n1g, r.n1b, h, B, HW, 1e-5f, true, stream, in_stats, in_stats_b);
   // conv1 + bias + time_emb_proj(silu(temb)) per (n, c)
   {
     dlm_conv_nhwc_args a{};
@@ -1162,26 +1171,35 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
                             kv_half, ctx_len, ctx_pad, B * ctx_len, kv_total_, c.cross_dim, stream));
 
   size_t ri = 0, ai = 0;
-  std::vector<std::pair<void*, int>> skips;
+  // down-path outputs the up path concatenates, with their producers' GroupNorm
+  // statistics (null where not written)
+  struct Skip {
+    void* x;
+    int C;
+    void* st;
+  };
+  std::vector<Skip> skips;
   // ---- conv_in (latent NCHW -> channels-last, zero-padded to 64 channels)
   void* xin = P((size_t)B * HW0 * kConvInPad);
   LAUNCH(kOther, 0.0, 0.0, dlm_nchw_to_nhwc_fp16(latent, xin, B, c.in_channels, HW0, kConvInPad, stream));
-  // GroupNorm statistics written by the conv that produces a GroupNorm's
-  // single-source input (conv1 -> norm2 inside each resnet; here: conv_in,
-  // the downsamplers and resnet outputs that feed a GroupNorm directly)
+  // GroupNorm statistics written by the conv (or proj_out) that produces a
+  // GroupNorm's input (conv1 -> norm2 inside each resnet; here: conv_in, the
+  // downsamplers, resnet and transformer outputs that feed a GroupNorm, and
+  // both sources of every up-path concatenation: each skip and the h it is
+  // concatenated with)
   auto S = [&](int C, int HWs) { return gn_stats_ws(persist, B, C, HWs, gn_fold_); };
   void* cur = P((size_t)B * HW0 * C0);
   void* cur_st = S(C0, HW0);
   conv3(conv_in_, xin, kConvInPad, nullptr, 0, cur, C0, B, H, W, 1, false, stream, c.in_channels, cur_st);
   stage("conv_in_out", cur, (size_t)B * HW0 * C0, C0, stream);
-  skips.push_back({cur, C0});
+  skips.push_back({cur, C0, cur_st});
 
   // ---- down_blocks.0
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW0 * C0);
-    void* o_st = r == 0 ? S(C0, HW0) : nullptr;  // the second resnet's output feeds the downsampler
+    void* o_st = S(C0, HW0);  // the next norm1, or (second resnet) up_blocks.2's last concatenation
     resnet(res_[ri++], cur, C0, nullptr, 0, o, B, H, W, tproj, stream, cur_st, o_st);
-    skips.push_back({o, C0});
+    skips.push_back({o, C0, o_st});
     cur = o;
     cur_st = o_st;
   }
@@ -1189,20 +1207,20 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
     void* d = P((size_t)B * HW1 * C0);
     cur_st = S(C0, HW1);
     conv3(down0_, cur, C0, nullptr, 0, d, C0, B, H, W, 2, false, stream, -1, cur_st);
-    skips.push_back({d, C0});
+    skips.push_back({d, C0, cur_st});
     cur = d;
   }
   stage("down_block_0_out", cur, (size_t)B * HW1 * C0, C0, stream);
-  // ---- down_blocks.1 (the first transformer's proj_out writes the second
-  // resnet's norm1 statistics; the second's output feeds the downsampler)
+  // ---- down_blocks.1 (each transformer's proj_out writes the statistics of
+  // its output: the second resnet's norm1, and both skips)
   int curC = C0;
   for (int r = 0; r < 2; ++r) {
     void* o = P((size_t)B * HW1 * C1);
     void* o_st = S(C1, HW1);
-    void* t_st = r == 0 ? S(C1, HW1) : nullptr;
+    void* t_st = S(C1, HW1);
     resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H1, W1, tproj, stream, cur_st, o_st);
     t2d(t2d_[ai++], o, B, HW1, ckv, ctx_len, stream, o_st, t_st);
-    skips.push_back({o, C1});
+    skips.push_back({o, C1, t_st});
     cur = o;
     cur_st = t_st;
     curC = C1;
@@ -1211,7 +1229,7 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
     void* d = P((size_t)B * HW2 * C1);
     cur_st = S(C1, HW2);
     conv3(down1_, cur, C1, nullptr, 0, d, C1, B, H1, W1, 2, false, stream, -1, cur_st);
-    skips.push_back({d, C1});
+    skips.push_back({d, C1, cur_st});
     cur = d;
   }
   stage("down_block_1_out", cur, (size_t)B * HW2 * C1, C1, stream);
@@ -1224,7 +1242,7 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
     void* t_st = S(C2, HW2);
     resnet(res_[ri++], cur, curC, nullptr, 0, o, B, H2, W2, tproj, stream, cur_st, o_st);
     t2d(t2d_[ai++], o, B, HW2, ckv, ctx_len, stream, o_st, t_st);
-    skips.push_back({o, C2});
+    skips.push_back({o, C2, t_st});
     cur = o;
     cur_st = t_st;
     curC = C2;
@@ -1238,8 +1256,10 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
     resnet(res_[ri++], cur, C2, nullptr, 0, m0, B, H2, W2, tproj, stream, cur_st, m0_st);
     t2d(t2d_[ai++], m0, B, HW2, ckv, ctx_len, stream, m0_st, t_st);
     void* m1 = P((size_t)B * HW2 * C2);
-    resnet(res_[ri++], m0, C2, nullptr, 0, m1, B, H2, W2, tproj, stream, t_st);
+    void* m1_st = S(C2, HW2);  // h of up_blocks.0's first concatenation
+    resnet(res_[ri++], m0, C2, nullptr, 0, m1, B, H2, W2, tproj, stream, t_st, m1_st);
     cur = m1;
+    cur_st = m1_st;
   }
   stage("mid_block_out", cur, (size_t)B * HW2 * C2, C2, stream);
   // ---- up_blocks
@@ -1249,22 +1269,29 @@ void UNet::forward_impl(int B, int H, int W, const void* latent, const float* d_
   for (int u = 0; u < 3; ++u) {
     const int Hh = upH[u], Ww = upW[u], HWu = Hh * Ww, C = upC[u];
     for (int r = 0; r < 3; ++r) {
-      const auto sk = skips.back();
+      const Skip sk = skips.back();
       skips.pop_back();
       void* o = P((size_t)B * HWu * C);
-      // a transformer's GroupNorm, or conv_norm_out after the last resnet
-      void* o_st = depth[u] > 0 || (u == 2 && r == 2) ? S(C, HWu) : nullptr;
-      resnet(res_[ri++], cur, curC, sk.first, sk.second, o, B, Hh, Ww, tproj, stream, nullptr, o_st);
-      if (depth[u] > 0) t2d(t2d_[ai++], o, B, HWu, ckv, ctx_len, stream, o_st);
+      // the output's next GroupNorm: the transformer's, the next
+      // concatenation's (h), or conv_norm_out
+      void* o_st = S(C, HWu);
+      resnet(res_[ri++], cur, curC, sk.x, sk.C, o, B, Hh, Ww, tproj, stream, cur_st, o_st, sk.st);
+      cur_st = o_st;
+      if (depth[u] > 0) {
+        // the transformer rewrites o in place; its proj_out writes the
+        // statistics of the next concatenation's h (none before the upsampler)
+        void* t_st = r < 2 ? S(C, HWu) : nullptr;
+        t2d(t2d_[ai++], o, B, HWu, ckv, ctx_len, stream, o_st, t_st);
+        cur_st = t_st;
+      }
       cur = o;
-      cur_st = depth[u] > 0 ? nullptr : o_st;  // the transformer rewrote o in place
       curC = C;
     }
     if (u < 2) {
       void* up = P((size_t)B * 4 * HWu * C);
-      conv3(u == 0 ? up0_ : up1_, cur, C, nullptr, 0, up, C, B, Hh, Ww, 1, true, stream);
+      cur_st = S(C, 4 * HWu);  // h of the next up block's first concatenation
+      conv3(u == 0 ? up0_ : up1_, cur, C, nullptr, 0, up, C, B, Hh, Ww, 1, true, stream, -1, cur_st);
       cur = up;
-      cur_st = nullptr;
     }
     static const char* names[3] = {"up_block_0_out", "up_block_1_out", "up_block_2_out"};
     const int HWo = u < 2 ? 4 * HWu : HWu;

@@ -244,7 +244,7 @@ class UNet {
   // its producer, or null; out_stats: where conv2 writes those of out, or null
   void resnet(const Resnet& r, const void* xa, int Ca, const void* xb, int Cb, void* out, int B,
               int H, int W, const void* tproj, void* stream, const void* in_stats = nullptr,
-              void* out_stats = nullptr);
+              void* out_stats = nullptr, const void* in_stats_b = nullptr);
   // every block's cross-attention K ([B*ctx, sumC]) and V^T ([B, sumC, ld])
   struct CrossKV {
     void* k;
@@ -266,7 +266,8 @@ class UNet {
   // prestats: a GroupNorm workspace whose chunk statistics of xa (no xb)
   // its producer wrote (dlm_conv_nhwc_args::gn_stats), or null
   void gn(const void* xa, int Ca, const void* xb, int Cb, const void* g, const void* b, void* out,
-          int B, int HW, float eps, bool silu, void* stream, const void* prestats = nullptr);
+          int B, int HW, float eps, bool silu, void* stream, const void* prestats = nullptr,
+          const void* prestats_b = nullptr);
   void conv3(const Conv& c, const void* x, int C, const void* xb, int Cb, void* out, int Co, int B,
              int H, int W, int stride, bool up, void* stream, int flop_cin = -1,
              void* gn_stats = nullptr);

@@ -312,30 +312,32 @@ __device__ __forceinline__ double gn_block_sum(double v, double* red) {
 // round trip per loop iteration each.  Larger groups read global memory in
 // both passes.  Same sums in the same order either way.
 constexpr int kGnFinStage = 8192;
+// The statistics of channels [0, Ca) are read from sa ([N][chunks][Ca]), those
+// of [Ca, C) from sb ([N][chunks][C - Ca]): a channel concatenation's two
+// sources, each with its own producer's statistics.  One source: Ca = C.
 __global__ void __launch_bounds__(256)
-gn_chan_finalize_kernel(const float2* __restrict__ stats, int HW, int C, int G, int chunks,
-                        const f16* __restrict__ gamma, const f16* __restrict__ beta, float eps,
-                        float2* __restrict__ ss) {
+gn_chan_finalize_kernel(const float2* __restrict__ sa, int Ca, const float2* __restrict__ sb, int HW,
+                        int C, int G, int chunks, const f16* __restrict__ gamma,
+                        const f16* __restrict__ beta, float eps, float2* __restrict__ ss) {
   __shared__ float2 ent[kGnFinStage];
   __shared__ double red[4];
   const int n = blockIdx.x / G, g = blockIdx.x % G;
   const int cpg = C / G;
+  const int Cb = C - Ca;
   const int total = chunks * cpg;
-  const float2* base = stats + (size_t)n * chunks * C + g * cpg;
+  auto load = [&](int j) -> float2 {
+    const int k = j / cpg;
+    const int c = g * cpg + (j - k * cpg);
+    const size_t row = (size_t)n * chunks + k;
+    return c < Ca ? sa[row * Ca + c] : sb[row * Cb + (c - Ca)];
+  };
   const bool staged = total <= kGnFinStage;
   if (staged) {
 #pragma unroll 8
-    for (int j = threadIdx.x; j < total; j += 256) {
-      const int k = j / cpg;
-      ent[j] = base[(size_t)k * C + (j - k * cpg)];
-    }
+    for (int j = threadIdx.x; j < total; j += 256) ent[j] = load(j);
     __syncthreads();
   }
-  auto entry = [&](int j) -> float2 {
-    if (staged) return ent[j];
-    const int k = j / cpg;
-    return base[(size_t)k * C + (j - k * cpg)];
-  };
+  auto entry = [&](int j) -> float2 { return staged ? ent[j] : load(j); };
   // pixels in entry j's chunk: 64, except in a partial last chunk
   const int last0 = (chunks - 1) * cpg;
   const double nlast = (double)(HW - (chunks - 1) * kGnChunk);
@@ -438,7 +440,8 @@ template <typename T>
 static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
                              const void* gamma, const void* beta, void* out, int ld_out, int N,
                              int HW, int C, int G, float eps, int silu, void* ws, hipStream_t s,
-                             bool prestats = false) {
+                             bool prestats = false, const float2* stats_a = nullptr,
+                             const float2* stats_b = nullptr) {
   const GnPlan p = gn_plan(N, C, HW);
   float2* partial = (float2*)ws;
   float2* ss = gn_ss_of(ws, N, C, HW);
@@ -452,8 +455,12 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
       const int st = gn_chan_stats_launch((const f16*)a, C_a, ld_a, (const f16*)b, ld_b, N, HW, C, partial, s);
       if (st != DLM_OK) return st;
     }
-    DLM_LAUNCH("gn_chan_finalize_kernel", gn_chan_finalize_kernel, dim3(N * G), dim3(256), 0, s, partial, HW, C,
-               G, gn_chan_chunks(HW), (const f16*)gamma, (const f16*)beta, eps, ss);
+    // producer statistics of two sources (stats_b), or of one source, or the
+    // statistics pass's, in the workspace
+    const float2* sa = stats_b ? stats_a : partial;
+    const int Ca = stats_b ? C_a : C;
+    DLM_LAUNCH("gn_chan_finalize_kernel", gn_chan_finalize_kernel, dim3(N * G), dim3(256), 0, s, sa, Ca, stats_b,
+               HW, C, G, gn_chan_chunks(HW), (const f16*)gamma, (const f16*)beta, eps, ss);
     DLM_LAUNCH_CHECK();
   } else {
     if (prestats) return fail(DLM_ERR_UNSUPPORTED, "group_norm: chunk statistics need fp16 input of <= 16384 pixels");
@@ -485,11 +492,11 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
 int group_norm_nhwc(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
                     const void* gamma, const void* beta, void* out, int ld_out, int N, int HW,
                     int C, int G, float eps, int silu, void* ws, hipStream_t s, bool in_f32 = false,
-                    bool prestats = false) {
+                    bool prestats = false, const float2* stats_a = nullptr, const float2* stats_b = nullptr) {
   return in_f32 ? group_norm_nhwc_t<float>(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N,
                                            HW, C, G, eps, silu, ws, s, prestats)
                 : group_norm_nhwc_t<f16>(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N,
-                                         HW, C, G, eps, silu, ws, s, prestats);
+                                         HW, C, G, eps, silu, ws, s, prestats, stats_a, stats_b);
 }
 
 // ---------------------------------------------------------------------------
@@ -654,6 +661,27 @@ int dlm_group_norm_nhwc_prestats_fp16(const void* in, int ld_in, const void* gam
               "buffers must be 16-byte aligned");
   return group_norm_nhwc(in, C, ld_in, nullptr, 0, gamma, beta, out, ld_out, N, HW, C, num_groups, eps,
                          fuse_silu, workspace, (hipStream_t)stream, false, true);
+}
+
+int dlm_group_norm_nhwc_prestats2_fp16(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
+                                       const void* stats_a, const void* stats_b, const void* gamma,
+                                       const void* beta, void* out, int ld_out, int N, int HW, int C,
+                                       int num_groups, float eps, int fuse_silu, void* workspace,
+                                       void* stream) {
+  if (N <= 0 || HW <= 0 || C <= 0 || num_groups <= 0) return DLM_OK;
+  DLM_REQUIRE(in_a && in_b && stats_a && stats_b && out && workspace, "NULL pointer");
+  DLM_REQUIRE(C % num_groups == 0, "C must be divisible by num_groups");
+  DLM_REQUIRE(C % 8 == 0 && C_a % 8 == 0 && C_a > 0 && C_a < C, "C and C_a must be multiples of 8, 0 < C_a < C");
+  DLM_REQUIRE(HW <= kGnChanMaxHW, "chunk statistics cover at most 16384 pixels per sample");
+  DLM_REQUIRE(ld_a % 8 == 0 && ld_a >= C_a && ld_b % 8 == 0 && ld_b >= C - C_a && ld_out % 8 == 0 &&
+                  ld_out >= C,
+              "bad row strides");
+  DLM_REQUIRE(dlm_aligned16(in_a) && dlm_aligned16(in_b) && dlm_aligned16(out) && dlm_aligned16(workspace) &&
+                  ((uintptr_t)stats_a & 7) == 0 && ((uintptr_t)stats_b & 7) == 0,
+              "buffers must be 16-byte aligned (statistics 8-byte)");
+  return group_norm_nhwc(in_a, C_a, ld_a, in_b, ld_b, gamma, beta, out, ld_out, N, HW, C, num_groups, eps,
+                         fuse_silu, workspace, (hipStream_t)stream, false, true, (const float2*)stats_a,
+                         (const float2*)stats_b);
 }
 
 int dlm_group_norm_chunk_stats_fp16(const void* in, int ld_in, int N, int HW, int C, void* workspace,

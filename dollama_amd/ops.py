@@ -567,6 +567,29 @@ def group_norm_nhwc_prestats(x: torch.Tensor, gamma, beta, groups: int, eps: flo
     return out
 
 
+def group_norm_nhwc_prestats2(x: torch.Tensor, x_b: torch.Tensor, gamma, beta, groups: int, eps: float,
+                              silu: bool, ws_a: torch.Tensor, ws_b: torch.Tensor, out=None) -> torch.Tensor:
+    """GroupNorm of concat(x [N,H,W,Ca], x_b [N,H,W,Cb]) from each source's chunk
+    statistics (the first bytes of ws_a, ws_b: GroupNorm workspaces for Ca and
+    Cb channels)."""
+    N, H, W, Ca = x.shape
+    Cb = x_b.shape[3]
+    C, HW = Ca + Cb, H * W
+    _need(x, N * HW * Ca, "x")
+    _need(x_b, N * HW * Cb, "x_b")
+    _need(gamma, C, "gamma", optional=True)
+    _need(beta, C, "beta", optional=True)
+    _need(ws_a, group_norm_workspace_bytes(N, Ca, HW), "ws_a", dtype=torch.uint8)
+    _need(ws_b, group_norm_workspace_bytes(N, Cb, HW), "ws_b", dtype=torch.uint8)
+    if out is None:
+        out = torch.empty(N, H, W, C, dtype=torch.float16, device=x.device)
+    _need(out, N * HW * C, "out")
+    ws = group_norm_workspace(N, C, HW, x.device)
+    call("dlm_group_norm_nhwc_prestats2_fp16", _p(x), Ca, Ca, _p(x_b), Cb, _p(ws_a), _p(ws_b), _p(gamma),
+         _p(beta), _p(out), C, N, HW, C, groups, float(eps), int(silu), _p(ws), stream_handle())
+    return out
+
+
 def attention_strided(q, k, v, o, *, B, H, Sq, Sk, q_strides, k_strides, v_strides, o_strides,
                       scale, Dh=64):
     """Flash attention with (batch, token, head) strides in elements per tensor."""

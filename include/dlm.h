@@ -397,6 +397,21 @@ int dlm_group_norm_chunk_stats_fp16(const void* in, int ld_in, int N, int HW, in
 int dlm_group_norm_nhwc_prestats_fp16(const void* in, int ld_in, const void* gamma, const void* beta,
                                       void* out, int ld_out, int N, int HW, int C, int num_groups,
                                       float eps, int fuse_silu, void* workspace, void* stream);
+/* The same over the channel concatenation of two fp16 sources (in_a's C_a
+ * channels, then in_b's C - C_a), each with its own chunk statistics:
+ * stats_a [N][chunks][C_a] and stats_b [N][chunks][C - C_a], as their
+ * producers wrote them (the first bytes of a GroupNorm workspace for that
+ * source's channel count).  workspace (dlm_group_norm_nhwc_workspace_bytes(N,
+ * C, HW)) receives the scale / shift only.  Same result as
+ * dlm_group_norm_nhwc_fp16 over the two sources, bit for bit.  The UNet's
+ * up-path ResnetBlock2D norm1 over concat(h, skip); the reference
+ * concatenates first and normalises the copy (src/infer/unet.cu:1168-1181,
+ * k_concat_chw at :247-277). */
+int dlm_group_norm_nhwc_prestats2_fp16(const void* in_a, int C_a, int ld_a, const void* in_b, int ld_b,
+                                       const void* stats_a, const void* stats_b, const void* gamma,
+                                       const void* beta, void* out, int ld_out, int N, int HW, int C,
+                                       int num_groups, float eps, int fuse_silu, void* workspace,
+                                       void* stream);
 /* Same GroupNorm(+SiLU) over fp32 channels-last input (one source), fp16
  * output: the VAE decoder's fp32 stages (reference launch_group_norm_f32,
  * src/kernels/vae_decode.cu:466-545). */

@@ -124,6 +124,29 @@ def test_group_norm_chunk_statistics_vs_oracle(gpu, N, C, H, W, mean, std):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("N,Ca,Cb,H,W,G", [(2, 640, 320, 16, 16, 32), (2, 1280, 640, 8, 8, 32),
+                                          (1, 40, 24, 9, 7, 4), (3, 320, 320, 12, 10, 32)])
+def test_group_norm_concat_from_two_sources_statistics(gpu, N, Ca, Cb, H, W, G):
+    """GroupNorm(+SiLU) over concat(xa, xb) from each source's own chunk
+    statistics (dlm_group_norm_nhwc_prestats2_fp16, the UNet's up-path norm1)
+    equals the GroupNorm that computes the concatenation's statistics itself,
+    bit for bit: UNet level shapes, a group that straddles the two sources
+    (40 + 24 channels in groups of 16), and a partial last chunk."""
+    announce(f"group_norm concat prestats N={N} Ca={Ca} Cb={Cb} {H}x{W} G={G}")
+    xa = ops.nchw_to_nhwc(to_gpu(randn((N, Ca, H, W), 700 + Ca, std=1.5, mean=0.3)))
+    xb = ops.nchw_to_nhwc(to_gpu(randn((N, Cb, H, W), 701 + Cb, std=0.7, mean=-2.0)))
+    C = Ca + Cb
+    gm, bt = to_gpu(randn((C,), 702, std=0.3, mean=1.0)), to_gpu(randn((C,), 703, std=0.3))
+    wa = ops.group_norm_chunk_stats(xa, ops.group_norm_workspace(N, Ca, H * W, gpu))
+    wb = ops.group_norm_chunk_stats(xb, ops.group_norm_workspace(N, Cb, H * W, gpu))
+    for silu in (True, False):
+        y1 = ops.group_norm_nhwc_prestats2(xa, xb, gm, bt, G, 1e-5, silu, wa, wb)
+        y2 = ops.group_norm_nhwc(xa, gm, bt, G, 1e-5, silu, x_b=xb)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), f"silu={silu}: two-source statistics differ from the pass"
+
+
+@pytest.mark.gpu
 def test_conv_gn_stats_argument_checks(gpu):
     """gn_stats is refused with an NCHW or fp32 output."""
     x, wp, b, _ = _conv_case(1, 64, 8, 8, 64, 1, 500)
