@@ -220,9 +220,11 @@ __global__ void __launch_bounds__(256) flash_attn_d64_kernel(AttnParams p) {
 //     feeds to one P^T fragment belong to eight consecutive keys: the matching
 //     V^T fragment is then 16 contiguous bytes of a V^T row;
 //   * each wave owns one block of 32 queries;
-//   * the running max is kept on raw scores, p = 2^(s*c - m*c) is one FMA and
-//     one v_exp_f32 (c = scale * log2 e); masking runs only on a partial last
-//     key tile.
+//   * Q is multiplied by c = scale * log2 e once, and every score chain starts
+//     its MFMA accumulator at -m (the lane's base), so p = 2^s is one
+//     v_exp_f32; the base moves only when a tile's P would overflow fp16 (a
+//     rare branch, see the softmax), so there is no per-tile max; masking
+//     runs only on a partial last key tile.
 // ===========================================================================
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 #define DLM_LDS __attribute__((address_space(3)))
