@@ -424,6 +424,44 @@ def test_attention_vt_rebase_paths(gpu, mode, B, H, Sq, Sk):
     assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), f"attention_vt {mode}")
 
 
+@pytest.mark.parametrize("mode", ["first", "late", "spike"])
+@pytest.mark.parametrize("B,H,Sq,Sk", [(1, 2, 1024, 1024), (1, 64, 1024, 1024), (1, 2, 300, 333)])
+def test_attention_vt_overflow_rebase(gpu, mode, B, H, Sq, Sk):
+    """The flash kernel's base moves only when some p = 2^(s - m) of a tile
+    would overflow fp16 (s - m >= 16 in the exponent's units): scores whose
+    first tile already overflows (Q x 16: a spread of ~23 per score), keys whose scores
+    grow by ~35 along the sequence (the base moves up on many tiles), and one
+    key in a late tile whose score jumps ~40 above all others.  Both
+    query-block widths (2 heads: 64-query workgroups; 64 heads: 128-query
+    workgroups) and a partial last tile.  Same bar as every attention case."""
+    Dh = 64
+    C = H * Dh
+    announce(f"attention_vt overflow rebase {mode} B={B} H={H} Sq={Sq} Sk={Sk}")
+    q, k, v = randn((B, H, Sq, Dh), 150), randn((B, H, Sk, Dh), 151), randn((B, H, Sk, Dh), 152)
+    if mode == "first":
+        q = (q * 16).half().float()
+    elif mode == "late":  # key j's score grows like 24 j / Sk in raw units (~35 in log2 units)
+        q = (0.5 + 0.1 * q).half().float()
+        k = (torch.linspace(0.0, 6.0, Sk).reshape(1, 1, Sk, 1) + 0.1 * k).half().float()
+    else:  # key 3 Sk / 4 aligned with every query: raw score ~28 above the rest
+        q = (0.5 + 0.1 * q).half().float()
+        j = 3 * Sk // 4
+        k[:, :, j, :] = 7.0
+        k = k.half().float()
+    dq = to_gpu(q.permute(0, 2, 1, 3).reshape(B, Sq, C))
+    dk = to_gpu(k.permute(0, 2, 1, 3).reshape(B, Sk, C))
+    ld = (Sk + 7) // 8 * 8
+    vt = torch.zeros(B, H, Dh, ld, dtype=torch.float16, device=gpu)
+    vt[..., :Sk] = to_gpu(v.transpose(2, 3).contiguous())
+    o = torch.empty(B, Sq, C, dtype=torch.float16, device=gpu)
+    ops.attention_vt(dq, dk, vt, o, B=B, H=H, Sq=Sq, Sk=Sk, q_strides=(Sq * C, C, Dh),
+                     k_strides=(Sk * C, C, Dh), vt_strides=(H * Dh * ld, Dh * ld), vt_ld=ld,
+                     o_strides=(Sq * C, C, Dh), scale=0.125)
+    assert torch.isfinite(o).all(), f"attention_vt overflow {mode}: non-finite output"
+    ref = torch.cat([R.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], 0.125) for b in range(B)])
+    assert_close(o, ref.permute(0, 2, 1, 3).reshape(B, Sq, C), f"attention_vt overflow {mode}")
+
+
 @pytest.mark.parametrize("M,N,K,act,vt", [
     (2048, 1280, 1280, 0, False), (8192, 640, 640, 0, False), (2048, 3840, 1280, 0, True),
     (8192, 1920, 640, 0, True), (2048, 10240, 1280, 4, False), (8192, 5120, 640, 4, False),
