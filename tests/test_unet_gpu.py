@@ -117,13 +117,17 @@ def test_unet_groupnorm_statistics_fold_is_bit_exact(gpu):
     """GroupNorm statistics written by the producing convs' epilogues (the
     default) give the same noise_pred, bit for bit, as a statistics pass in
     every GroupNorm, eager and under graph replay, at a latent whose deepest
-    level (4x4) leaves a partial 64-pixel chunk."""
+    level (4x4) leaves a partial 64-pixel chunk, and at one whose top level
+    (136x136 = 18496 pixels) is past the 16384-pixel limit of the chunk
+    statistics (that level's GroupNorms, the up path's concatenations
+    included, run the statistics pass while the levels below take producer
+    statistics)."""
     cfg = TINY
     Wc = OR.random_weights(OR.TINY, seed=23)
     net = U.UNet(cfg)
     net.set_weights(_to_gpu(Wc))
     net.prepare()
-    for H in (32, 16):
+    for H in (136, 32, 16):
         print(f"[case] tiny UNet GroupNorm statistics fold on/off, latent {H}x{H}", flush=True)
         lat, ts, ehs, text, ids = _inputs(cfg, 2, H, H, 77, seed=24)
         args = (lat.half().cuda(), ts.cuda(), ehs.half().cuda(), text.half().cuda(), ids.half().cuda())
