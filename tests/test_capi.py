@@ -51,6 +51,34 @@ def test_invalid_arguments_are_rejected_without_a_device():
     assert b"NULL" in lib.dlm_last_error()
 
 
+def test_groupnorm_statistics_entries_reject_bad_arguments_without_a_device():
+    """The GroupNorm chunk-statistics entries check their arguments before any
+    device call: NULL operands, more pixels than the chunk statistics cover,
+    and a concatenation split outside (0, C)."""
+    lib = ctypes.CDLL(LIBS["dlm.h"])
+    lib.dlm_last_error.restype = ctypes.c_char_p
+    P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    lib.dlm_group_norm_chunk_stats_fp16.argtypes = [P, I, I, I, I, P, P]
+    lib.dlm_group_norm_nhwc_prestats_fp16.argtypes = [P, I, P, P, P, I, I, I, I, I, F, I, P, P]
+    lib.dlm_group_norm_nhwc_prestats2_fp16.argtypes = [P, I, I, P, I, P, P, P, P, P, I, I, I, I, I, F, I, P, P]
+    fake = 1 << 20  # aligned, never dereferenced: every case fails its checks first
+    assert lib.dlm_group_norm_chunk_stats_fp16(None, 64, 2, 64, 64, fake, None) == 1
+    assert lib.dlm_group_norm_chunk_stats_fp16(fake, 64, 2, 16385, 64, fake, None) == 1
+    assert b"16384" in lib.dlm_last_error()
+    assert lib.dlm_group_norm_nhwc_prestats_fp16(None, 64, None, None, fake, 64, 2, 64, 64, 32, 1e-5, 1,
+                                                 fake, None) == 1
+    # concat: NULL second source, then C_a outside (0, C)
+    assert lib.dlm_group_norm_nhwc_prestats2_fp16(fake, 32, 32, None, 32, fake, fake, None, None, fake, 64,
+                                                  2, 64, 64, 32, 1e-5, 1, fake, None) == 1
+    assert b"NULL" in lib.dlm_last_error()
+    assert lib.dlm_group_norm_nhwc_prestats2_fp16(fake, 64, 64, fake, 8, fake, fake, None, None, fake, 64,
+                                                  2, 64, 64, 32, 1e-5, 1, fake, None) == 1
+    assert b"C_a" in lib.dlm_last_error()
+    # non-positive dims stay a silent no-op
+    assert lib.dlm_group_norm_nhwc_prestats2_fp16(None, 32, 32, None, 32, None, None, None, None, None, 64,
+                                                  0, 64, 64, 32, 1e-5, 1, None, None) == 0
+
+
 def test_host_library_pure_host_entry_points():
     from dollama_amd import unet as U
     specs = U.weight_specs(U.SDXL_CONFIG)
