@@ -291,36 +291,44 @@ gn_chan_stats_kernel(const f16* __restrict__ a, int Ca, int lda, const f16* __re
   }
 }
 
-// Merge of the per-channel chunk statistics of one (n, group), one 256-thread
-// block each, in fp64 by the same two-pass decomposition as
+// Merge of the per-channel chunk statistics of one (n, group), one block of
+// kGnFinT threads each, in fp64 by the same two-pass decomposition as
 // gn_finalize_kernel; entry j = (chunk j / cpg, channel j % cpg) of the
-// group; per-thread sums in order, then the wave reduction (the same value
-// in every lane) and the four waves' results added in wave order, so every
+// group.  Per-thread sums in order, then the wave reduction (the same value
+// in every lane) and the waves' results added in a fixed tree, so every
 // thread holds the same, launch-invariant result.
+constexpr int kGnFinT = 1024;
+constexpr int kGnFinW = kGnFinT / 64;
 __device__ __forceinline__ double gn_block_sum(double v, double* red) {
   v = wave_sum_f64(v);
   const int wave = threadIdx.x >> 6;
   __syncthreads();  // red free (an earlier sum's readers are done)
   if ((threadIdx.x & 63) == 0) red[wave] = v;
   __syncthreads();
-  return ((red[0] + red[1]) + red[2]) + red[3];
+  double t[kGnFinW / 2];
+#pragma unroll
+  for (int i = 0; i < kGnFinW / 2; ++i) t[i] = red[2 * i] + red[2 * i + 1];
+#pragma unroll
+  for (int w = kGnFinW / 4; w >= 1; w /= 2)
+#pragma unroll
+    for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+  return t[0];
 }
 
-// A (sample, group) of up to kGnFinStage entries (every UNet GroupNorm:
-// at most 256 chunks x 30 channels) is first copied into LDS, every load in
-// flight at once; the two passes then read LDS instead of making one global
-// round trip per loop iteration each.  Larger groups read global memory in
-// both passes.  Same sums in the same order either way.
-constexpr int kGnFinStage = 8192;
+// A (sample, group) of up to kGnFinT * kGnFinE entries (every UNet GroupNorm:
+// at most 256 chunks x 30 channels) is loaded once into registers, every
+// load in flight together, and both passes run over the registers: one
+// global round trip per launch.  Larger groups read global memory in both
+// passes, in the same per-thread order.
+constexpr int kGnFinE = 8;
 // The statistics of channels [0, Ca) are read from sa ([N][chunks][Ca]), those
 // of [Ca, C) from sb ([N][chunks][C - Ca]): a channel concatenation's two
 // sources, each with its own producer's statistics.  One source: Ca = C.
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kGnFinT)
 gn_chan_finalize_kernel(const float2* __restrict__ sa, int Ca, const float2* __restrict__ sb, int HW,
                         int C, int G, int chunks, const f16* __restrict__ gamma,
                         const f16* __restrict__ beta, float eps, float2* __restrict__ ss) {
-  __shared__ float2 ent[kGnFinStage];
-  __shared__ double red[4];
+  __shared__ double red[kGnFinW];
   const int n = blockIdx.x / G, g = blockIdx.x % G;
   const int cpg = C / G;
   const int Cb = C - Ca;
@@ -331,32 +339,49 @@ gn_chan_finalize_kernel(const float2* __restrict__ sa, int Ca, const float2* __r
     const size_t row = (size_t)n * chunks + k;
     return c < Ca ? sa[row * Ca + c] : sb[row * Cb + (c - Ca)];
   };
-  const bool staged = total <= kGnFinStage;
-  if (staged) {
-#pragma unroll 8
-    for (int j = threadIdx.x; j < total; j += 256) ent[j] = load(j);
-    __syncthreads();
-  }
-  auto entry = [&](int j) -> float2 { return staged ? ent[j] : load(j); };
   // pixels in entry j's chunk: 64, except in a partial last chunk
   const int last0 = (chunks - 1) * cpg;
   const double nlast = (double)(HW - (chunks - 1) * kGnChunk);
   auto count = [&](int j) { return j >= last0 ? nlast : (double)kGnChunk; };
   const double cnt = (double)HW * cpg;
-  double s1 = 0.0;
-  for (int j = threadIdx.x; j < total; j += 256) s1 = fma(count(j), (double)entry(j).x, s1);
-  s1 = gn_block_sum(s1, red);
-  const double mean = s1 / cnt;
-  double m2 = 0.0;
-  for (int j = threadIdx.x; j < total; j += 256) {
-    const float2 q = entry(j);
-    const double d = (double)q.x - mean;
-    m2 += (double)q.y + count(j) * d * d;
+  const int tid = threadIdx.x;
+  double s1 = 0.0, m2 = 0.0, mean;
+  if (total <= kGnFinT * kGnFinE) {
+    float2 q[kGnFinE];
+#pragma unroll
+    for (int i = 0; i < kGnFinE; ++i) {
+      const int j = tid + i * kGnFinT;
+      q[i] = j < total ? load(j) : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < kGnFinE; ++i) {
+      const int j = tid + i * kGnFinT;
+      if (j < total) s1 = fma(count(j), (double)q[i].x, s1);
+    }
+    s1 = gn_block_sum(s1, red);
+    mean = s1 / cnt;
+#pragma unroll
+    for (int i = 0; i < kGnFinE; ++i) {
+      const int j = tid + i * kGnFinT;
+      if (j < total) {
+        const double d = (double)q[i].x - mean;
+        m2 += (double)q[i].y + count(j) * d * d;
+      }
+    }
+  } else {
+    for (int j = tid; j < total; j += kGnFinT) s1 = fma(count(j), (double)load(j).x, s1);
+    s1 = gn_block_sum(s1, red);
+    mean = s1 / cnt;
+    for (int j = tid; j < total; j += kGnFinT) {
+      const float2 q = load(j);
+      const double d = (double)q.x - mean;
+      m2 += (double)q.y + count(j) * d * d;
+    }
   }
   m2 = gn_block_sum(m2, red);
   const double var = fmax(m2 / cnt, 0.0);
   const float rstd = (float)(1.0 / sqrt(var + (double)eps));
-  for (int ci = threadIdx.x; ci < cpg; ci += 256) {
+  for (int ci = tid; ci < cpg; ci += kGnFinT) {
     const int c = g * cpg + ci;
     const float gm = gamma ? (float)gamma[c] : 1.0f;
     const float bt = beta ? (float)beta[c] : 0.0f;
@@ -459,7 +484,7 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
     // statistics pass's, in the workspace
     const float2* sa = stats_b ? stats_a : partial;
     const int Ca = stats_b ? C_a : C;
-    DLM_LAUNCH("gn_chan_finalize_kernel", gn_chan_finalize_kernel, dim3(N * G), dim3(256), 0, s, sa, Ca, stats_b,
+    DLM_LAUNCH("gn_chan_finalize_kernel", gn_chan_finalize_kernel, dim3(N * G), dim3(kGnFinT), 0, s, sa, Ca, stats_b,
                HW, C, G, gn_chan_chunks(HW), (const f16*)gamma, (const f16*)beta, eps, ss);
     DLM_LAUNCH_CHECK();
   } else {
