@@ -390,12 +390,11 @@ gn_chan_finalize_kernel(const float2* __restrict__ sa, int Ca, const float2* __r
   }
 }
 
-// Apply: same blocks as the statistics pass (one chunk of one sample's
-// pixels, S * R threads).  A thread owns one 8-channel vector for the whole
-// chunk: its source (concat half), scale and shift are fixed, so they are
-// resolved once and stay in registers, and the loop keeps four pixel rows in
-// flight per thread.
-template <typename T, bool SILU>
+// Apply: one chunk of one sample's pixels per block, S * R threads.  A
+// thread owns one 8-channel vector for the whole chunk: its source (concat
+// half), scale and shift are fixed, so they are resolved once and stay in
+// registers, and the loop keeps U pixel rows in flight per thread.
+template <typename T, bool SILU, int U>
 __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
                                 const T* __restrict__ b, int ldb, f16* __restrict__ out,
                                 int ldo, int HW, int C, int S, int R, int chunk,
@@ -426,13 +425,13 @@ __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
     sc[2 * i + 1] = q.z;
     sh[2 * i + 1] = q.w;
   }
-  for (int p = p0 + r; p < p1; p += 4 * R) {
-    float x[4][8];
+  for (int p = p0 + r; p < p1; p += U * R) {
+    float x[U][8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < U; ++u)
       if (p + u * R < p1) load8(src + (size_t)(p + u * R) * ld, x[u]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       if (p + u * R < p1) {
         f16x8 y;
 #pragma unroll
@@ -504,12 +503,26 @@ static int group_norm_nhwc_t(const void* in_a, int C_a, int ld_a, const void* in
                           ? "gn_partial_kernel+gn_finalize_kernel+gn_apply_kernel"
                           : (prestats ? "gn_chan_finalize_kernel+gn_apply_kernel"
                                       : "gn_chan_stats_kernel+gn_chan_finalize_kernel+gn_apply_kernel");
-  if (silu)
-    DLM_LAUNCH(label, gn_apply_kernel<T, true>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b, ld_b,
-               (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss);
-  else
-    DLM_LAUNCH(label, gn_apply_kernel<T, false>, dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b, ld_b,
-               (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss);
+  // Apply blocks: the statistics pass's (four rows in flight per thread)
+  // where that pass ran; after chunk statistics, whose 64-pixel chunks do
+  // not constrain it, two rows per thread and twice the blocks (GN + SiLU from
+  // producer statistics: 2x128^2x320 14.8 -> 13.7 us, 2x64^2x1920 18.1 ->
+  // 17.2 us; 2x64^2x640 10.0 -> 10.2 us).
+  if (std::is_same<T, f16>::value && HW <= kGnChanMaxHW) {
+    const int chunk = std::max(p.R * 2, (HW + 1023) / 1024), chunks = (HW + chunk - 1) / chunk;
+    if (silu)
+      DLM_LAUNCH(label, (gn_apply_kernel<T, true, 2>), dim3(chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b,
+                 ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, chunk, ss);
+    else
+      DLM_LAUNCH(label, (gn_apply_kernel<T, false, 2>), dim3(chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b,
+                 ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, chunk, ss);
+  } else if (silu) {
+    DLM_LAUNCH(label, (gn_apply_kernel<T, true, 4>), dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b,
+               ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss);
+  } else {
+    DLM_LAUNCH(label, (gn_apply_kernel<T, false, 4>), dim3(p.chunks, N), dim3(p.threads), 0, s, a, C_a, ld_a, b,
+               ld_b, (f16*)out, ld_out, HW, C, p.S, p.R, p.chunk, ss);
+  }
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }
