@@ -332,21 +332,7 @@ flash_vt_pipe_kernel(FlashVtParams p) {
   const int g = lane >> 5;
   const int q0 = qb * (NWV * 32) + wave * 32;
 
-  // Q scaled by c = scale * log2(e) once (one fp16 rounding of q * c), so the
-  // scores come out of the MFMA in the exponent's units
-  f16x8 qf[4];
-  {
-    const int qi = q0 + (lane & 31);
-    const f16* qp = p.q + b * p.q_sb + h * p.q_sh + (long long)qi * p.q_ss + g * 8;
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      f16x8 v = qi < p.Sq ? *reinterpret_cast<const f16x8*>(qp + ds * 16) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] = (f16)((float)v[t] * p.c);
-      qf[ds] = v;
-    }
-  }
-
+  f16x8 qf[4];  // this wave's 32 queries, loaded below
   const i32x4 rk = fa_rsrc(p.k, p.k_bytes);
   const i32x4 rv = fa_rsrc(p.vt, p.vt_bytes);
   // DMA instruction i of this wave: LDS row r of the tile, 16-byte chunk c of
@@ -413,6 +399,31 @@ flash_vt_pipe_kernel(FlashVtParams p) {
   const int nkt = (p.Sk + FA_TK - 1) / FA_TK;
   issue(0, 0);
   if (nkt > 1) issue(1, 1);
+
+  // Q scaled by c = scale * log2(e) once (one fp16 rounding of q * c), so the
+  // scores come out of the MFMA in the exponent's units.  Loaded after the
+  // first tiles' DMA is issued, so the two latencies overlap (loaded first,
+  // the scaling's wait held the DMA back by one memory round trip).
+  // Rows past Sq load row Sq - 1 and scale it by 0: no branch around the
+  // loads (the compiler copies, and waits for, a load's result inside one).
+  // A padded row's scores stay in its own lane and its output is never
+  // stored.
+  {
+    const int qi = q0 + (lane & 31);
+    const bool qin = qi < p.Sq;
+    const f16* qp = p.q + b * p.q_sb + h * p.q_sh + (long long)(qin ? qi : p.Sq - 1) * p.q_ss + g * 8;
+    f16x8 v[4];
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) v[ds] = *reinterpret_cast<const f16x8*>(qp + ds * 16);
+    const float cq = qin ? p.c : 0.0f;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[ds][t] = (f16)((float)v[ds][t] * cq);
+      qf[ds] = v[ds];
+    }
+  }
+
 
   // Running state, in log2 units: the scores of a tile arrive as s - m with m
   // the lane's current base (negm = -m broadcast is every score chain's
