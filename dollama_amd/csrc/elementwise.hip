@@ -117,7 +117,11 @@ __global__ void sdxl_embed_kernel(const float* timesteps, const f16* text, int t
   }
 }
 
-// Skinny linear (M <= 16): one wave per output column, W row streamed once.
+// Skinny linear (M <= MB <= 16): one wave per output column, W row streamed
+// once.  The MB rows' loads are unconditional (rows past M re-read row
+// M - 1, never stored), so each k-step issues all its loads before waiting:
+// a load under a lane branch is copied, and waited for, inside it.
+template <int MB>
 __global__ void __launch_bounds__(256)
 linear_small_kernel(const f16* __restrict__ X, int ldx, const f16* __restrict__ W,
                     const f16* __restrict__ bias, f16* __restrict__ Y, int ldy, int M, int N,
@@ -125,28 +129,28 @@ linear_small_kernel(const f16* __restrict__ X, int ldx, const f16* __restrict__ 
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
-  float acc[16];
+  float acc[MB];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) acc[m] = 0.0f;
+  for (int m = 0; m < MB; ++m) acc[m] = 0.0f;
   const f16* w = W + (size_t)n * K;
   for (int k = lane * 8; k < K; k += 512) {
     const f16x8 wv = *reinterpret_cast<const f16x8*>(w + k);
+    f16x8 xv[MB];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      if (m < M) {
-        const f16x8 xv = *reinterpret_cast<const f16x8*>(X + (size_t)m * ldx + k);
+    for (int m = 0; m < MB; ++m) xv[m] = *reinterpret_cast<const f16x8*>(X + (size_t)min(m, M - 1) * ldx + k);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float xf = (float)xv[i];
-          if (silu_in) xf = silu_f(xf);
-          acc[m] += xf * (float)wv[i];
-        }
+    for (int m = 0; m < MB; ++m) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float xf = (float)xv[m][i];
+        if (silu_in) xf = silu_f(xf);
+        acc[m] += xf * (float)wv[i];
       }
     }
   }
   const float bn = bias ? (float)bias[n] : 0.0f;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
+  for (int m = 0; m < MB; ++m) {
     if (m < M) {
       float v = wave_sum(acc[m]) + bn;
       if (act == DLM_ACT_SILU) v = silu_f(v);
@@ -378,9 +382,19 @@ int dlm_linear_small_fp16(const void* X, int ldx, const void* W, const void* bia
   DLM_REQUIRE(K % 8 == 0 && ldx % 8 == 0 && ldx >= K && ldy >= N, "bad K / strides");
   DLM_REQUIRE(dlm_aligned16(X) && dlm_aligned16(W), "X and W must be 16-byte aligned");
   DLM_REQUIRE(act == DLM_ACT_NONE || act == DLM_ACT_SILU, "act must be none or silu");
-  DLM_LAUNCH("linear_small_kernel", linear_small_kernel, dim3((N + 3) / 4), dim3(256), 0, (hipStream_t)stream,
-                     (const f16*)X, ldx, (const f16*)W, (const f16*)bias, (f16*)Y, ldy, M, N, K,
-                     silu_in, act, accumulate);
+#define DLM_LINEAR_SMALL(MB)                                                                               \
+  DLM_LAUNCH("linear_small_kernel", linear_small_kernel<MB>, dim3((N + 3) / 4), dim3(256), 0,                  \
+             (hipStream_t)stream, (const f16*)X, ldx, (const f16*)W, (const f16*)bias, (f16*)Y, ldy, M, N, K, \
+             silu_in, act, accumulate)
+  if (M <= 2)
+    DLM_LINEAR_SMALL(2);
+  else if (M <= 4)
+    DLM_LINEAR_SMALL(4);
+  else if (M <= 8)
+    DLM_LINEAR_SMALL(8);
+  else
+    DLM_LINEAR_SMALL(16);
+#undef DLM_LINEAR_SMALL
   DLM_LAUNCH_CHECK();
   return DLM_OK;
 }

@@ -415,8 +415,18 @@ __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
   }
   src += (size_t)n * HW * ld;
   f16* dst = out + (size_t)n * HW * ldo + c;
-  float sc[8], sh[8];
   const float4* ssv = reinterpret_cast<const float4*>(ss + (size_t)n * C + c);
+  int p = p0 + r;
+  if (p >= p1) return;
+  // The first trip's rows, then the scale / shift, all issued before any is
+  // waited for: rows past the chunk re-read its last row (never stored)
+  // instead of skipping the load, since a load under a lane branch is copied,
+  // and waited for, inside it; and a scale / shift loaded ahead of the loop
+  // would be waited for at its head, before the rows are requested.
+  float x[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) load8(src + (size_t)min(p + u * R, p1 - 1) * ld, x[u]);
+  float sc[8], sh[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float4 q = ssv[i];
@@ -425,11 +435,7 @@ __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
     sc[2 * i + 1] = q.z;
     sh[2 * i + 1] = q.w;
   }
-  for (int p = p0 + r; p < p1; p += U * R) {
-    float x[U][8];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (p + u * R < p1) load8(src + (size_t)(p + u * R) * ld, x[u]);
+  while (true) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (p + u * R < p1) {
@@ -443,6 +449,10 @@ __global__ void gn_apply_kernel(const T* __restrict__ a, int Ca, int lda,
         *reinterpret_cast<f16x8*>(dst + (size_t)(p + u * R) * ldo) = y;
       }
     }
+    p += U * R;
+    if (p >= p1) break;
+#pragma unroll
+    for (int u = 0; u < U; ++u) load8(src + (size_t)min(p + u * R, p1 - 1) * ld, x[u]);
   }
 }
 
@@ -555,24 +565,27 @@ layer_norm_kernel(const f16* __restrict__ in, const f16* __restrict__ gamma,
   // 6.2 -> 5.5 us); narrower rows load them after the statistics (8192 x 640
   // measured 5% slower with the early loads).
   constexpr bool kEarly = VPL >= 3;
-  float v[VPL][8];
-  f16x8 gh[VPL], bh[VPL];
+  // Every load of the row is issued before any is waited for: lanes past
+  // the row's end re-read its last vector (never used) instead of skipping
+  // the load, since a load under a lane branch has its result copied, and
+  // waited for, inside the branch, one memory round trip per vector.
+  f16x8 xh[VPL], gh[VPL], bh[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int s = lane + 64 * j;
-    if (s < S) {
-      load8(x + s * 8, v[j]);
-      if (kEarly && gamma) gh[j] = *reinterpret_cast<const f16x8*>(gamma + s * 8);
-      if (kEarly && beta) bh[j] = *reinterpret_cast<const f16x8*>(beta + s * 8);
-    }
+    const int s = min(lane + 64 * j, S - 1);
+    xh[j] = *reinterpret_cast<const f16x8*>(x + s * 8);
+    if (kEarly && gamma) gh[j] = *reinterpret_cast<const f16x8*>(gamma + s * 8);
+    if (kEarly && beta) bh[j] = *reinterpret_cast<const f16x8*>(beta + s * 8);
   }
+  float v[VPL][8];
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int s = lane + 64 * j;
-    if (s < S) {
+    const bool in = lane + 64 * j < S;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum += v[j][i];
+    for (int i = 0; i < 8; ++i) {
+      v[j][i] = in ? (float)xh[j][i] : 0.0f;
+      sum += v[j][i];
     }
   }
   const float mean = wave_sum(sum) / (float)C;
@@ -588,13 +601,19 @@ layer_norm_kernel(const f16* __restrict__ in, const f16* __restrict__ gamma,
       }
     }
   }
+  if constexpr (!kEarly) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int s = min(lane + 64 * j, S - 1);
+      if (gamma) gh[j] = *reinterpret_cast<const f16x8*>(gamma + s * 8);
+      if (beta) bh[j] = *reinterpret_cast<const f16x8*>(beta + s * 8);
+    }
+  }
   const float rstd = rsqrtf(wave_sum(sq) / (float)C + eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int s = lane + 64 * j;
     if (s < S) {
-      if (!kEarly && gamma) gh[j] = *reinterpret_cast<const f16x8*>(gamma + s * 8);
-      if (!kEarly && beta) bh[j] = *reinterpret_cast<const f16x8*>(beta + s * 8);
       f16x8 y;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
