@@ -297,7 +297,7 @@ gn_chan_stats_kernel(const f16* __restrict__ a, int Ca, int lda, const f16* __re
 // group.  Per-thread sums in order, then the wave reduction (the same value
 // in every lane) and the waves' results added in a fixed tree, so every
 // thread holds the same, launch-invariant result.
-constexpr int kGnFinT = 1024;
+constexpr int kGnFinT = 512;
 constexpr int kGnFinW = kGnFinT / 64;
 __device__ __forceinline__ double gn_block_sum(double v, double* red) {
   v = wave_sum_f64(v);
@@ -320,7 +320,7 @@ __device__ __forceinline__ double gn_block_sum(double v, double* red) {
 // load in flight together, and both passes run over the registers: one
 // global round trip per launch.  Larger groups read global memory in both
 // passes, in the same per-thread order.
-constexpr int kGnFinE = 8;
+constexpr int kGnFinE = 16;
 // The statistics of channels [0, Ca) are read from sa ([N][chunks][Ca]), those
 // of [Ca, C) from sb ([N][chunks][C - Ca]): a channel concatenation's two
 // sources, each with its own producer's statistics.  One source: Ca = C.
