@@ -105,15 +105,15 @@ def test_linear_gn_stats_equal_stats_pass(gpu, tile):
 @pytest.mark.gpu
 @pytest.mark.parametrize("N,C,H,W,mean,std", [(2, 320, 128, 128, 0.0, 1.0), (2, 640, 64, 64, 40.0, 0.5),
                                               (1, 1280, 32, 32, -3.0, 2.0), (3, 64, 9, 7, 0.5, 1.5),
-                                              (1, 1280, 127, 121, 1.0, 1.0)])
+                                              (1, 1024, 128, 128, 0.0, 1.0), (1, 1280, 127, 121, 1.0, 1.0)])
 def test_group_norm_chunk_statistics_vs_oracle(gpu, N, C, H, W, mean, std):
     """GroupNorm(+SiLU) over the chunk statistics (the path of every fp16
     GroupNorm of up to 16384 pixels) against the float64 oracle on the same
     fp16 values, at the UNet's three level shapes, a mean 80x the standard
-    deviation, a pixel count that leaves a partial last chunk, and groups of
-    more entries (241 chunks x 40 channels) than the merge holds in
-    registers; the prestats form from the statistics pass gives the same
-    bits."""
+    deviation, a pixel count that leaves a partial last chunk, groups of
+    exactly as many entries as the merge holds in registers (256 chunks x 32
+    channels) and of more (241 chunks x 40 channels); the prestats form from
+    the statistics pass gives the same bits."""
     announce(f"group_norm chunk statistics N={N} C={C} {H}x{W} mean {mean} std {std}")
     x = randn((N, C, H, W), 90 + C, std=std, mean=mean)
     gm, bt = randn((C,), 91, std=0.3, mean=1.0), randn((C,), 92, std=0.3)

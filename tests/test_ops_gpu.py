@@ -290,7 +290,7 @@ def test_group_norm_many_samples(gpu):
 
 
 # ------------------------------------------------------------- LayerNorm ---
-@pytest.mark.parametrize("rows,C", [(8192, 640), (2048, 1280), (77, 2048), (5, 100)])
+@pytest.mark.parametrize("rows,C", [(8192, 640), (2048, 1280), (77, 2048), (5, 100), (13, 520), (3, 8), (6, 1032)])
 def test_layer_norm(gpu, rows, C):
     announce(f"launch_layer_norm rows={rows} C={C}")
     x = randn((rows, C), 90, std=1.5, mean=0.3)
@@ -574,6 +574,21 @@ def test_timestep_and_sdxl_embeddings(gpu):
     t_emb, add_in = ops.sdxl_embed_inputs(ts, to_gpu(text), to_gpu(ids))
     assert (from_gpu(t_emb) - R.timestep_embedding(torch.full((B,), 999.0), 320)).abs().max() < 2e-3
     assert (from_gpu(add_in) - R.add_embedding_input(text, ids)).abs().max() < 2e-3
+
+
+@pytest.mark.parametrize("M", [1, 3, 5, 16])
+def test_linear_small_row_bounds(gpu, M):
+    """Every row bound of the skinny linear (rows padded to 2, 4, 8, 16 load
+    the last real row, never stored), with a column count that leaves the
+    last block's waves partly idle, and the accumulate form."""
+    announce(f"linear_small M={M}")
+    x, w, b = randn((M, 520), 150 + M), randn((37, 520), 151, std=0.05), randn((37,), 152, std=0.01)
+    y = ops.linear_small(to_gpu(x), to_gpu(w), to_gpu(b))
+    assert_close(y, R.linear(x, w, b), f"linear_small M={M}")
+    base = randn((M, 37), 153)
+    y2 = to_gpu(base)
+    ops.linear_small(to_gpu(x), to_gpu(w), to_gpu(b), out=y2, accumulate=True)
+    assert_close(y2, R.linear(x, w, b) + base.half().float(), f"linear_small M={M} accumulate")
 
 
 def test_linear_small(gpu):
