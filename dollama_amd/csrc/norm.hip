@@ -299,6 +299,7 @@ gn_chan_stats_kernel(const f16* __restrict__ a, int Ca, int lda, const f16* __re
 // thread holds the same, launch-invariant result.
 constexpr int kGnFinT = 512;
 constexpr int kGnFinW = kGnFinT / 64;
+static_assert(kGnFinW >= 2 && (kGnFinW & (kGnFinW - 1)) == 0, "the tree adds a power of two of wave sums");
 __device__ __forceinline__ double gn_block_sum(double v, double* red) {
   v = wave_sum_f64(v);
   const int wave = threadIdx.x >> 6;
