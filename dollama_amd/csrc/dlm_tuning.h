@@ -31,7 +31,8 @@ extern "C" {
  * 36 128x80 16x80 2, 37 128x160 32x80 2, 38 128x128 64x32 2,
  * 39 128x64 64x32 3; 40 128x128 32x64 2 and 41 256x160 32x160 3 with the
  * next slice's first fragments read early; 42 128x16 16x16 3 and 43 64x16
- * 16x16 3 (outputs of at most 16 columns).  Splits apply to the LDS-DMA core
+ * 16x16 3 (outputs of at most 16 columns); 44 192x160 48x80 3 (at most 192
+ * rows, e.g. the text tokens' K/V projection).  Splits apply to the LDS-DMA core
  * only. */
 int dlm_gemm_force_tile(int tile_id);
 /* Same override for GEMMs / convs of one shape (M, N = output columns,

@@ -55,11 +55,11 @@ def test_linear_geglu(gpu, M, d, K):
     assert_close(y, R.geglu(R.linear(x, w, b)), f"geglu {M}x{d}x{K}")
 
 
-@pytest.mark.parametrize("tile", list(range(8, 44)))
+@pytest.mark.parametrize("tile", list(range(8, 45)))
 def test_dma_tile_configs(gpu, tile):
-    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-43, the
-    fragment-prefetch forms 27-34, two-slice stages 35-39 and the 16-column
-    tiles 42-43 included),
+    """Every LDS-DMA tile configuration (dlm_gemm_force_tile 8-44, the
+    fragment-prefetch forms 27-34, two-slice stages 35-39, the 16-column
+    tiles 42-43 and the 192-row tile 44 included),
     whole and split-K, on ragged shapes with an odd slice count and a K tail:
     bias + SiLU + residual, GEGLU, and a 3x3 conv with residual."""
     from dollama_amd import _lib
